@@ -1,0 +1,226 @@
+"""Benchmark of the attention hot path on one MI355X; prints ONE JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S]
+
+Headline (``value``): causal flash prefill, B=2, H=32, N=8192, D=128 fp16
+(where the north-star target is stated), in TFLOP/s with
+the reference's FLOP convention 4*B*H*N^2*D/2 (bench/bench.py:153).  A step is
+one prefill call over that batch with inputs already resident in HBM.
+
+The same line carries, under ``workloads``, the other BASELINE configs measured
+the same way: non-causal prefill, the N=8191 variant, and the two
+paged split-K decode configs in KV GB/s with the reference's byte convention
+sum(ctx)*Hkv*D*2*2 (bench/bench.py:199-200).
+
+``roofline`` is the headline kernel's algorithmic FLOP per launch divided by its
+mean launch duration (HIP events on the launch stream, inside the timed
+region), against the 2.5 PFLOP/s dense fp16 MFMA peak.  ``cpu_baseline`` times
+the numpy oracle (oracle/attention.py) on a bounded sample of the same
+workload on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "flash-attention-from-scratch_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def timed_steps(fn, steps, warmup):
+    """W untimed calls, then exactly K calls bracketed by synchronize; per-launch
+    HIP events on the current (launch) stream.  Returns (total_ms, mean_event_ms,
+    median_event_ms)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    total_ms = (time.perf_counter() - t0) * 1e3
+    ev = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    return total_ms, sum(ev) / len(ev), statistics.median(ev)
+
+
+def prefill_case(b, h, n, d, causal, steps, warmup, seed=0):
+    import numpy as np
+    import torch
+
+    import attnkernels as ak
+    import oracle
+
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    q, k, v = (torch.randn(b, h, n, d, generator=g, device="cuda", dtype=torch.float16) for _ in range(3))
+    fn = lambda: ak.flash_attention(q, k, v, causal=causal)  # noqa: E731
+    out = fn()
+    torch.cuda.synchronize()
+    ref = oracle.attention_fp32(*(t[0, 0].cpu().numpy() for t in (q, k, v)), causal)
+    err = float(np.abs(out[0, 0].float().cpu().numpy() - ref).max())
+    del out
+    total_ms, ev_mean, ev_med = timed_steps(fn, steps, warmup)
+    flops = oracle.prefill_flops(b, h, n, d, causal)
+    ms = total_ms / steps
+    res = dict(workload=f"prefill B={b} H={h} N={n} D={d} {'causal' if causal else 'non-causal'}",
+               value=round(flops / (ms * 1e-3) / 1e12, 2), unit="TFLOP/s", ms_per_step=round(ms, 4),
+               kernel_ms_mean=round(ev_mean, 4), kernel_ms_median=round(ev_med, 4),
+               kernel_tflops=round(flops / (ev_mean * 1e-3) / 1e12, 2),
+               frac_of_peak=round(flops / (ev_mean * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
+               flop_per_launch=flops, max_abs_err=float(f"{err:.3g}"))
+    del q, k, v
+    torch.cuda.empty_cache()
+    return res
+
+
+def decode_case(lens, hkv, d, bs, partition, steps, warmup, seed=0, hq=None):
+    import numpy as np
+    import torch
+
+    import attnkernels as ak
+    import oracle
+
+    hq = hkv if hq is None else hq
+    nblk = [-(-c // bs) for c in lens]
+    pool = -(-sum(nblk) * 11 // 10)
+    rng = np.random.default_rng(seed)
+    perm = rng.permutation(pool).astype(np.int32)
+    bt = np.zeros((len(lens), max(nblk)), np.int32)
+    pos = 0
+    for i, nb in enumerate(nblk):
+        bt[i, :nb] = perm[pos:pos + nb]
+        pos += nb
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    shape = (pool, hkv, bs, d)
+    kc = torch.randn(shape, generator=g, device="cuda", dtype=torch.float16)
+    vc = torch.randn(shape, generator=g, device="cuda", dtype=torch.float16)
+    q = torch.randn(len(lens), hq, d, generator=g, device="cuda", dtype=torch.float16)
+    btd = torch.from_numpy(bt).cuda()
+    cld = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    max_ctx = max(lens)
+    fn = lambda: ak.paged_decode(q, kc, vc, btd, cld, max_ctx, partition_size=partition)  # noqa: E731
+    out = fn()
+    torch.cuda.synchronize()
+    pages = torch.from_numpy(bt[0]).long().cuda()
+    ref = oracle.paged_decode_fp32(q[:1].cpu().numpy(), kc[pages].cpu().numpy(), vc[pages].cpu().numpy(),
+                                   np.arange(bt.shape[1], dtype=np.int32)[None], np.asarray(lens[:1]))
+    err = float(np.abs(out[:1].float().cpu().numpy() - ref).max())
+    del out
+    total_ms, ev_mean, ev_med = timed_steps(fn, steps, warmup)
+    nbytes = oracle.decode_kv_bytes(lens, hkv, d)
+    ms = total_ms / steps
+    res = dict(workload=f"paged decode B={len(lens)} Hq={hq} Hkv={hkv} D={d} bs={bs} P={partition} "
+                        f"sum_ctx={sum(lens)} max_ctx={max_ctx}",
+               value=round(nbytes / (ms * 1e-3) / 1e9, 1), unit="GB/s", ms_per_step=round(ms, 4),
+               kernel_ms_mean=round(ev_mean, 4), kernel_ms_median=round(ev_med, 4),
+               kernel_gbs=round(nbytes / (ev_mean * 1e-3) / 1e9, 1),
+               frac_of_peak=round(nbytes / (ev_mean * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+               bytes_per_step=nbytes, splits=-(-max_ctx // partition), max_abs_err=float(f"{err:.3g}"))
+    del kc, vc, q
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(seconds):
+    """The numpy fp32 oracle on (batch, head) slices of the headline workload,
+    on this host's cores, for about ``seconds`` of CPU work."""
+    import numpy as np
+
+    import oracle
+
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # noqa: BLE001
+        threads = os.cpu_count() or 1
+    n, d = 8192, 128
+    rng = np.random.default_rng(0)
+    q, k, v = (rng.standard_normal((n, d), dtype=np.float32).astype(np.float16) for _ in range(3))
+    oracle.attention_fp32(q[:512], k[:512], v[:512], True)  # warm the BLAS threads
+    done, t0 = 0, time.perf_counter()
+    while True:
+        oracle.attention_fp32(q, k, v, True)
+        done += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    el = time.perf_counter() - t0
+    flops = oracle.prefill_flops(1, done, n, d, True)
+    return dict(value=round(flops / el / 1e12, 5), unit="TFLOP/s", cores=int(threads), kind="port",
+                sample=f"{done} (batch, head) slices of causal N=8192 D=128 through the numpy fp32 "
+                       f"oracle, {el:.1f} s, os.cpu_count()={os.cpu_count()}")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--only", choices=["all", "prefill", "decode", "headline"], default="all")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(see DESIGN.md for how the kernels would shard); run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import attnkernels as ak
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    ak.load_extension()
+    torch.manual_seed(0)
+    K, W = args.steps, args.warmup
+    headline = prefill_case(2, 32, 8192, 128, True, K, W)
+    log(json.dumps(headline))
+    workloads = []
+    if args.only in ("all", "prefill"):
+        for cfg in [(4, 16, 2048, 64, False), (2, 32, 8191, 128, True)]:
+            workloads.append(prefill_case(*cfg, K, W))
+            log(json.dumps(workloads[-1]))
+    if args.only in ("all", "decode"):
+        lens4 = torch.randint(1, 4097, (64,), generator=torch.Generator().manual_seed(4)).tolist()
+        for lens, d, part in [(lens4, 128, 512), ([32768] * 8, 128, 256), ([32768] * 8, 64, 256)]:
+            workloads.append(decode_case(lens, 32, d, 16, part, K, W))
+            log(json.dumps(workloads[-1]))
+    cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
+    ach = headline["kernel_tflops"]
+    line = {
+        "metric": "prefill TFLOP/s (% MFMA peak); paged decode KV GB/s (% HBM peak)",
+        "value": headline["value"], "unit": "TFLOP/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": headline["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+        "config": {"workload": headline["workload"] + " (BASELINE configs[2])", "global_batch": 2,
+                   "seq_len": 8192, "heads": 32, "head_dim": 128, "causal": True, "parallelism": "none"},
+        "max_abs_err": headline["max_abs_err"],
+        "roofline": {"bound": "mfma", "achieved": ach, "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(ach / PEAK_FP16_TFLOPS, 4), "traffic": None,
+                     "kernel": "flash_prefill_kernel<128,true>",
+                     "kernel_ms_mean": headline["kernel_ms_mean"]},
+        "cpu_baseline": cpu,
+        "workloads": workloads,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

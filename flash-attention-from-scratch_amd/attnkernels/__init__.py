@@ -1,0 +1,137 @@
+"""Attention kernels for LLM inference, hand-written for AMD MI355X (gfx950, CDNA4).
+
+Drop-in for the ``attnkernels`` package of sonhoang/flash-attention-from-scratch
+(attnkernels/__init__.py): same functions, arguments, defaults and errors.
+
+Prefill (many query tokens per sequence):
+    naive_attention   softmax(scale Q K^T [+ causal mask]) V
+    flash_attention   same maths; variant "simt" or "wmma" as in the reference
+All three run one gfx950 flash kernel on the f16 MFMA matrix cores with fp32
+accumulation and an online softmax; none materialises the N x N scores.
+
+Decode (one query token per sequence) over a paged KV cache:
+    paged_decode      split-K ("flash-decoding") kernel plus an LSE-merge reduce
+
+The native code (``libattnkernels.so``, C-ABI in ``include/attnkernels.h``, and
+the torch glue module ``attnkernels_ext``) is built in-tree by
+``attnkernels.build`` for gfx950.  There is no fallback: without the built
+extension and a GPU the entry points raise.
+"""
+from __future__ import annotations
+
+import functools
+import importlib.util
+import math
+import os
+
+import torch
+
+__all__ = ["naive_attention", "flash_attention", "paged_decode", "decode_partition",
+           "load_extension"]
+
+CHUNK = 256  # partitions are multiples of it (reference attnkernels/__init__.py:29)
+
+# Default block_n of the "wmma" variant per head dim, kept from the reference
+# (attnkernels/__init__.py:31-33).  On gfx950 block_n is validated (32 or 64)
+# but the MFMA kernel uses its own key tile (64 keys for D=128, 128 for D=64).
+WMMA_BLOCK_N = {64: 64, 128: 64}
+
+
+@functools.lru_cache(maxsize=None)
+def load_extension():
+    """Import the in-tree ``attnkernels_ext`` module, building it first if absent."""
+    from . import build as _build
+
+    if not _build.is_built():
+        _build.build(verbose=os.environ.get("ATTN_VERBOSE") == "1")
+    path = _build.ext_path()
+    spec = importlib.util.spec_from_file_location(_build.EXT_NAME, path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def _check_prefill(q, k, v):
+    """Reference attnkernels/__init__.py:53-61 (same checks, same ValueErrors)."""
+    for t in (q, k, v):
+        if not (t.is_cuda and t.dtype == torch.float16 and t.dim() == 4):
+            raise ValueError("q, k, v must be fp16 CUDA tensors of shape [B, H, N, D]")
+    if not (q.shape == k.shape == v.shape):
+        raise ValueError("q, k, v must have the same shape (self-attention prefill)")
+    if q.shape[-1] not in (64, 128):
+        raise ValueError("head_dim must be 64 or 128")
+    return q.contiguous(), k.contiguous(), v.contiguous()
+
+
+def naive_attention(q, k, v, causal=False, scale=None):
+    """softmax(scale * Q K^T [+ causal mask]) V (reference attnkernels/__init__.py:64-68).
+
+    The reference keeps the scores in DRAM; here the same call runs the MFMA
+    flash kernel, so it needs no O(N^2) buffer.
+    """
+    q, k, v = _check_prefill(q, k, v)
+    scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
+    return load_extension().naive_attention(q, k, v, causal, scale)
+
+
+def flash_attention(q, k, v, causal=False, scale=None, variant="wmma", block_n=None):
+    """Tiled attention with online softmax. q, k, v: fp16 [B, H, N, D], D in {64, 128}.
+
+    variant: "simt" or "wmma" (both run the gfx950 MFMA kernel).
+    block_n: key-tile width accepted by "wmma" (32 or 64), as in the reference.
+    Reference: attnkernels/__init__.py:71-85.
+    """
+    q, k, v = _check_prefill(q, k, v)
+    scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
+    ext = load_extension()
+    if variant == "simt":
+        return ext.flash_simt(q, k, v, causal, scale)
+    if variant == "wmma":
+        bn = WMMA_BLOCK_N[q.shape[-1]] if block_n is None else block_n
+        return ext.flash_wmma(q, k, v, causal, scale, bn)
+    raise ValueError(f"unknown variant {variant!r}")
+
+
+@functools.lru_cache(maxsize=None)
+def _sm_count(device_index):
+    """Compute units of the device (multi_processor_count is the CU count on ROCm)."""
+    return torch.cuda.get_device_properties(device_index).multi_processor_count
+
+
+def decode_partition(batch, num_kv_heads, max_context_len, device=None):
+    """Tokens per split for paged_decode: enough splits for about 4 workgroups
+    per CU in total, at least one 256-token chunk per split
+    (reference attnkernels/__init__.py:93-101)."""
+    dev = torch.cuda.current_device() if device is None else device
+    blocks = batch * num_kv_heads
+    want = -(-4 * _sm_count(dev) // blocks)
+    max_chunks = -(-max_context_len // CHUNK)
+    splits = max(1, min(want, max_chunks))
+    return -(-max_chunks // splits) * CHUNK
+
+
+def paged_decode(q, k_cache, v_cache, block_tables, context_lens, max_context_len,
+                 scale=None, partition_size=None):
+    """Decode attention over a paged KV cache (reference attnkernels/__init__.py:104-128).
+
+    q:            [B, H, D] fp16, one query token per sequence
+    k_cache:      [num_blocks, H_kv, block_size, D] fp16 (v_cache the same)
+    block_tables: [B, max_blocks_per_seq] int32, physical block ids
+    context_lens: [B] int32, tokens of context per sequence (>= 1)
+    max_context_len: Python int, max(context_lens) (passed in to avoid a sync)
+    partition_size: tokens per split (multiple of 256). None picks one from the
+                  batch size; a value >= max_context_len disables split-K.
+    """
+    if not (q.dtype == k_cache.dtype == v_cache.dtype == torch.float16):
+        raise ValueError("q and caches must be fp16")
+    if q.shape[-1] not in (64, 128) or k_cache.shape[-1] != q.shape[-1]:
+        raise ValueError("head_dim must be 64 or 128 and match the cache")
+    scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
+    if partition_size is None:
+        partition_size = decode_partition(q.shape[0], k_cache.shape[1], max_context_len,
+                                          q.device.index)
+    partition_size = -(-int(partition_size) // CHUNK) * CHUNK
+    return load_extension().paged_decode(
+        q.contiguous(), k_cache.contiguous(), v_cache.contiguous(),
+        block_tables.to(torch.int32).contiguous(), context_lens.to(torch.int32).contiguous(),
+        int(max_context_len), float(scale), partition_size)

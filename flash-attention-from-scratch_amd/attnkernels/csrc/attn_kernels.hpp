@@ -1,0 +1,44 @@
+// Internal launch interface between the C-ABI layer (capi.cpp) and the HIP
+// kernels (prefill.hip, decode.hip).  Arguments are validated by the caller.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace ak {
+
+struct PrefillArgs {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    int64_t bh;      // batch * heads
+    int64_t n;       // sequence length
+    int d;           // head dim, 64 or 128
+    bool causal;
+    float sl2;       // |scale| * log2(e)
+    uint32_t qflip;  // 0x80008000 when scale < 0 (sign folded into Q), else 0
+    void* stream;
+};
+
+struct DecodeArgs {
+    const void* q;         // [B, hq, D] fp16
+    const void* k_cache;   // [num_blocks, hkv, bs, D] fp16
+    const void* v_cache;
+    const int32_t* block_tables;  // [B, max_blocks]
+    const int32_t* context_lens;  // [B]
+    void* out;             // [B, hq, D] fp16
+    float* o_part;         // [B, hq, S, D]  (S > 1 only)
+    float* m_part;         // [B, hq, S]
+    float* l_part;         // [B, hq, S]
+    int64_t batch, hq, hkv, d, num_blocks, bs, max_blocks;
+    int64_t partition, num_splits;
+    float sl2;             // scale * log2(e)
+    void* stream;
+};
+
+hipError_t prefill_launch(const PrefillArgs& a);
+hipError_t decode_launch(const DecodeArgs& a);
+
+}  // namespace ak

@@ -1,0 +1,164 @@
+// C-ABI entry points (include/attnkernels.h): argument validation, the
+// reference's error wording, and dispatch to the HIP launchers.  Validation
+// runs before any HIP call, so a rejected call never touches the GPU.
+#include <climits>
+#include <cmath>
+#include <cstdio>
+#include <string>
+
+#include "attn_kernels.hpp"
+#include "attnkernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+constexpr double kLog2e = 1.4426950408889634;
+constexpr int64_t kChunk = 256;  // partitions are multiples of it (paged_decode.cu:37)
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int ok() {
+    g_last_error.clear();
+    return AK_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int hip_status(hipError_t e, const char* who) {
+    if (e == hipSuccess) return ok();
+    return fail(AK_ERR_HIP, std::string(who) + ": HIP error: " + hipGetErrorString(e));
+}
+
+int prefill(const char* who, const void* q, const void* k, const void* v, void* o, int64_t batch,
+            int64_t heads, int64_t seq_len, int64_t head_dim, int causal, double scale, void* stream) {
+    if (batch < 0 || heads < 0 || seq_len < 0)
+        return fail(AK_ERR_INVALID_ARGUMENT, std::string(who) + ": negative size");
+    if (batch * heads * seq_len == 0) return ok();  // empty output, nothing to launch
+    if (!q || !k || !v || !o) return fail(AK_ERR_INVALID_ARGUMENT, std::string(who) + ": null pointer");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+        return fail(AK_ERR_INVALID_ARGUMENT, std::string(who) + ": pointers must be 16-byte aligned");
+    if (seq_len > INT_MAX / 2 || batch * heads > INT_MAX)
+        return fail(AK_ERR_INVALID_ARGUMENT, std::string(who) + ": size out of range");
+    ak::PrefillArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.o = o;
+    a.bh = batch * heads;
+    a.n = seq_len;
+    a.d = (int)head_dim;
+    a.causal = causal != 0;
+    a.sl2 = (float)(std::fabs(scale) * kLog2e);
+    a.qflip = std::signbit(scale) && scale != 0.0 ? 0x80008000u : 0u;
+    a.stream = stream;
+    return hip_status(ak::prefill_launch(a), who);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ak_last_error(void) { return g_last_error.c_str(); }
+
+int ak_abi_version(void) { return 100; }
+
+int ak_naive_attention(const void* q, const void* k, const void* v, void* o, int64_t batch,
+                       int64_t heads, int64_t seq_len, int64_t head_dim, int causal, double scale,
+                       void* stream) {
+    if (head_dim != 64 && head_dim != 128)
+        return fail(AK_ERR_UNSUPPORTED, "naive_attention: head_dim must be 64 or 128");
+    return prefill("naive_attention", q, k, v, o, batch, heads, seq_len, head_dim, causal, scale, stream);
+}
+
+int ak_flash_simt(const void* q, const void* k, const void* v, void* o, int64_t batch, int64_t heads,
+                  int64_t seq_len, int64_t head_dim, int causal, double scale, void* stream) {
+    if (head_dim != 64 && head_dim != 128)
+        return fail(AK_ERR_UNSUPPORTED, "flash_simt: head_dim must be 64 or 128");
+    return prefill("flash_simt", q, k, v, o, batch, heads, seq_len, head_dim, causal, scale, stream);
+}
+
+int ak_flash_wmma(const void* q, const void* k, const void* v, void* o, int64_t batch, int64_t heads,
+                  int64_t seq_len, int64_t head_dim, int causal, double scale, int64_t block_n,
+                  void* stream) {
+    if ((head_dim != 64 && head_dim != 128) || (block_n != 32 && block_n != 64))
+        return fail(AK_ERR_UNSUPPORTED, "flash_wmma: head_dim must be 64 or 128 and block_n 32 or 64");
+    return prefill("flash_wmma", q, k, v, o, batch, heads, seq_len, head_dim, causal, scale, stream);
+}
+
+size_t ak_paged_decode_workspace_size(int64_t batch, int64_t num_heads, int64_t head_dim,
+                                      int64_t max_context_len, int64_t partition) {
+    if (batch < 0 || num_heads < 0 || head_dim <= 0 || max_context_len < 1 || partition <= 0) return 0;
+    const int64_t splits = (max_context_len + partition - 1) / partition;
+    if (splits <= 1) return 0;
+    return (size_t)batch * (size_t)num_heads * (size_t)splits * (size_t)(head_dim + 2) * sizeof(float);
+}
+
+int ak_paged_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_tables,
+                    const int32_t* context_lens, void* out, int64_t batch, int64_t num_heads,
+                    int64_t num_kv_heads, int64_t head_dim, int64_t num_blocks, int64_t block_size,
+                    int64_t max_blocks_per_seq, int64_t max_context_len, double scale, int64_t partition,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+    // Checks in the reference's order (paged_decode.cu:260-262, 275).
+    if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0)
+        return fail(AK_ERR_INVALID_ARGUMENT, "num_heads must be a multiple of num_kv_heads");
+    if (partition <= 0 || partition % kChunk != 0)
+        return fail(AK_ERR_INVALID_ARGUMENT, "partition size must be a positive multiple of 256");
+    const int64_t G = num_heads / num_kv_heads;
+    if ((head_dim != 64 && head_dim != 128) || (G != 1 && G != 2 && G != 4 && G != 8))
+        return fail(AK_ERR_UNSUPPORTED,
+                    "paged_decode: head_dim must be 64/128 and num_heads/num_kv_heads in {1,2,4,8}");
+    if (batch < 0 || num_blocks < 0 || block_size <= 0 || max_blocks_per_seq < 0)
+        return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: invalid size");
+    if (batch == 0) return ok();
+    if (max_context_len < 1)
+        return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: max_context_len must be >= 1");
+    if (max_blocks_per_seq < 1 || num_blocks < 1)
+        return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: empty block table or cache");
+    if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !out)
+        return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: null pointer");
+    if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
+        return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: q, caches and out must be 16-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(block_tables) & 3u) || (reinterpret_cast<uintptr_t>(context_lens) & 3u))
+        return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: int32 arrays must be 4-byte aligned");
+    if (max_context_len > INT_MAX - partition || partition > INT_MAX || num_blocks > INT_MAX ||
+        max_blocks_per_seq * block_size > INT_MAX || batch > 65535 || num_kv_heads > 65535)
+        return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: size out of range");
+    const int64_t splits = (max_context_len + partition - 1) / partition;
+    ak::DecodeArgs a{};
+    if (splits > 1) {
+        const size_t need = ak_paged_decode_workspace_size(batch, num_heads, head_dim, max_context_len, partition);
+        if (!workspace || workspace_bytes < need)
+            return fail(AK_ERR_WORKSPACE, "paged_decode: workspace of " + std::to_string(need) +
+                                              " bytes required, got " + std::to_string(workspace_bytes));
+        if (!aligned16(workspace))
+            return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: workspace must be 16-byte aligned");
+        float* ws = static_cast<float*>(workspace);
+        const size_t rows = (size_t)batch * (size_t)num_heads * (size_t)splits;
+        a.o_part = ws;
+        a.m_part = ws + rows * (size_t)head_dim;
+        a.l_part = a.m_part + rows;
+    }
+    a.q = q;
+    a.k_cache = k_cache;
+    a.v_cache = v_cache;
+    a.block_tables = block_tables;
+    a.context_lens = context_lens;
+    a.out = out;
+    a.batch = batch;
+    a.hq = num_heads;
+    a.hkv = num_kv_heads;
+    a.d = head_dim;
+    a.num_blocks = num_blocks;
+    a.bs = block_size;
+    a.max_blocks = max_blocks_per_seq;
+    a.partition = partition;
+    a.num_splits = splits;
+    a.sl2 = (float)(scale * kLog2e);
+    a.stream = stream;
+    return hip_status(ak::decode_launch(a), "paged_decode");
+}
+
+}  // extern "C"

@@ -1,0 +1,252 @@
+// Paged-KV split-K decode ("flash-decoding") and its LSE-merge reduce, gfx950.
+//
+// Same contract as the reference's kernel pair (paged_decode.cu:39-216): the
+// cache is [num_blocks, hkv, bs, D], token t of sequence b lives in page
+// block_tables[b][t / bs] at offset t % bs; a workgroup handles one
+// (split, kv head, sequence) and all G query heads that share the kv head, so
+// every K/V byte is read once; it writes the normalised partial o and (m, l) in
+// the log2 domain, or the fp16 output directly when there is one split; the
+// reduce merges partials with M = max m_s, w_s = l_s 2^(m_s - M),
+// O = sum w_s o_s / sum w_s.
+//
+// The kernel is built for HBM bandwidth, with no matrix cores:
+//   * a token row of one page is D*2 contiguous bytes; D/8 lanes cover it with
+//     one 16-byte load each, so one wave-wide load reads 4 (D=128) or 8 (D=64)
+//     tokens = 1 KB, and each lane keeps 8 K loads and 8 V loads in flight;
+//   * the dot product is v_dot2_f32_f16 on the raw fp16 q and k, reduced over
+//     the D/8 lanes of a token with DPP row permutes, then scaled by
+//     scale*log2(e) in fp32;
+//   * each group of D/8 lanes runs its own online softmax over the tokens it
+//     loads (no cross-lane traffic in the loop); the groups of a wave and the
+//     4 waves of a workgroup are merged once, at the end, by the same LSE rule.
+#include "attn_kernels.hpp"
+#include "wave.hpp"
+
+namespace ak {
+
+template <int D>
+struct DecodeTile {
+    static constexpr int NW = 4;                // waves per workgroup
+    static constexpr int THREADS = NW * kWave;  // 256
+    static constexpr int LPT = D / 8;           // lanes per token row
+    static constexpr int TPL = kWave / LPT;     // tokens per wave-wide load
+    static constexpr int U = 8;                 // loads in flight per lane, per cache
+    static constexpr int TOK = U * TPL;         // tokens per wave iteration
+};
+
+__device__ __forceinline__ float dot8(f16x8 a, f16x8 b) {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const f16x2 x = {a[2 * j], a[2 * j + 1]};
+        const f16x2 y = {b[2 * j], b[2 * j + 1]};
+        s = __builtin_amdgcn_fdot2(x, y, s, false);
+    }
+    return s;
+}
+
+template <int D, int G>
+__global__ void __launch_bounds__(256)
+paged_decode_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const f16* __restrict__ vc,
+                    const int* __restrict__ block_tables, const int* __restrict__ ctx_lens,
+                    f16* __restrict__ out, float* __restrict__ o_part, float* __restrict__ m_part,
+                    float* __restrict__ l_part, int hkv, int bs, int bs_shift, int max_blocks,
+                    int num_blocks, int partition, int num_splits, float sl2) {
+    using T = DecodeTile<D>;
+    __shared__ float red_acc[T::NW][G][D];
+    __shared__ float red_m[T::NW][G], red_l[T::NW][G];
+
+    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int hq = hkv * G;
+    const int ctx = min(ctx_lens[b], max_blocks * bs);  // never index past the table row
+    const int start = split * partition;
+    if (start >= ctx) return;  // whole workgroup: this split is past the context
+    const int end = min(ctx, start + partition);
+    const int tid = threadIdx.x, lane = tid & 63, w = uniform(tid >> 6);
+    const int gi = lane / T::LPT, li = lane % T::LPT;
+
+    // q for the G heads of this kv head, raw fp16 (scaled after the dot product).
+    f16x8 qv[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+        qv[h] = *reinterpret_cast<const f16x8*>(q + ((size_t)b * hq + kvh * G + h) * D + li * 8);
+
+    float m[G], l[G], acc[G][8];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        m[h] = -INFINITY;
+        l[h] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[h][i] = 0.f;
+    }
+    const int* bt = block_tables + (size_t)b * max_blocks;
+    const size_t page_stride = (size_t)hkv * bs * D;
+    const size_t head_off = (size_t)kvh * bs * D + li * 8;
+
+    for (int t0 = start + w * T::TOK; t0 < end; t0 += T::NW * T::TOK) {
+        f16x8 kr[T::U], vr[T::U];
+        bool valid[T::U];
+#pragma unroll
+        for (int u = 0; u < T::U; ++u) {
+            const int t = t0 + u * T::TPL + gi;
+            bool ok = t < end;
+            size_t off = 0;
+            if (ok) {
+                const int pi = bs_shift >= 0 ? (t >> bs_shift) : (t / bs);
+                const int po = t - pi * bs;
+                const int page = bt[pi];
+                ok = (unsigned)page < (unsigned)num_blocks;  // a bad page id is never read
+                off = (size_t)page * page_stride + head_off + (size_t)po * D;
+            }
+            valid[u] = ok;
+            kr[u] = ok ? *reinterpret_cast<const f16x8*>(kc + off) : f16x8{};
+            vr[u] = ok ? *reinterpret_cast<const f16x8*>(vc + off) : f16x8{};
+        }
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float s[T::U];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int u = 0; u < T::U; ++u) {
+                const float dsum = group_sum<T::LPT>(dot8(qv[h], kr[u]));
+                s[u] = valid[u] ? dsum * sl2 : -INFINITY;
+                mx = fmaxf(mx, s[u]);
+            }
+            const float m_new = fmaxf(m[h], mx);
+            const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+            const float alpha = exp2_fast(m[h] - m_use);
+            float psum = 0.f;
+#pragma unroll
+            for (int u = 0; u < T::U; ++u) {
+                s[u] = exp2_fast(s[u] - m_use);
+                psum += s[u];
+            }
+            l[h] = l[h] * alpha + psum;
+            m[h] = m_new;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float a = acc[h][i] * alpha;
+#pragma unroll
+                for (int u = 0; u < T::U; ++u) a = fmaf(s[u], (float)vr[u][i], a);
+                acc[h][i] = a;
+            }
+        }
+    }
+
+    // Merge the token groups of the wave (lanes that share li), then the waves.
+#pragma unroll
+    for (int off = T::LPT; off < kWave; off <<= 1) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            const float mo = __shfl_xor(m[h], off, kWave);
+            const float lo = __shfl_xor(l[h], off, kWave);
+            const float M = fmaxf(m[h], mo);
+            const float Mu = (M == -INFINITY) ? 0.f : M;
+            const float ws = exp2_fast(m[h] - Mu), wo = exp2_fast(mo - Mu);
+            l[h] = l[h] * ws + lo * wo;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[h][i] = acc[h][i] * ws + __shfl_xor(acc[h][i], off, kWave) * wo;
+            m[h] = M;
+        }
+    }
+    if (gi == 0) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) red_acc[w][h][li * 8 + i] = acc[h][i];
+            if (li == 0) {
+                red_m[w][h] = m[h];
+                red_l[w][h] = l[h];
+            }
+        }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < G * D; idx += T::THREADS) {
+        const int h = idx / D, d = idx % D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < T::NW; ++v) M = fmaxf(M, red_m[v][h]);
+        float L = 0.f, o = 0.f;
+#pragma unroll
+        for (int v = 0; v < T::NW; ++v) {
+            const float wv = exp2_fast(red_m[v][h] - M);  // waves without tokens: 2^-inf = 0
+            L += red_l[v][h] * wv;
+            o += red_acc[v][h][d] * wv;
+        }
+        o /= L;
+        const size_t row = (size_t)b * hq + kvh * G + h;
+        if (num_splits == 1) {
+            out[row * D + d] = (f16)o;
+        } else {
+            o_part[(row * num_splits + split) * D + d] = o;
+            if (d == 0) {
+                m_part[row * num_splits + split] = M;
+                l_part[row * num_splits + split] = L;
+            }
+        }
+    }
+}
+
+// One wave per (sequence, query head).  ns = ceil(ctx/P) partials are merged
+// (paged_decode.cu:204-215); ns is clamped to the number of launched splits.
+template <int D>
+__global__ void __launch_bounds__(64)
+paged_reduce_kernel(const float* __restrict__ o_part, const float* __restrict__ m_part,
+                    const float* __restrict__ l_part, const int* __restrict__ ctx_lens,
+                    f16* __restrict__ out, int hq, int partition, int num_splits) {
+    constexpr int PER = D / kWave;
+    const size_t row = blockIdx.x;
+    const int b = (int)(row / hq);
+    const int ctx = ctx_lens[b];
+    const int lane = threadIdx.x;
+    int ns = ctx > 0 ? (int)(((long long)ctx + partition - 1) / partition) : 0;
+    ns = min(ns, num_splits);
+    const float* mp = m_part + row * num_splits;
+    const float* lp = l_part + row * num_splits;
+    const float* op = o_part + row * num_splits * D;
+    float M = -INFINITY;
+    for (int s = 0; s < ns; ++s) M = fmaxf(M, mp[s]);
+    float num[PER], den = 0.f;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) num[j] = 0.f;
+    for (int s = 0; s < ns; ++s) {
+        const float wgt = lp[s] * exp2_fast(mp[s] - M);
+#pragma unroll
+        for (int j = 0; j < PER; ++j) num[j] = fmaf(wgt, op[(size_t)s * D + lane + j * kWave], num[j]);
+        den += wgt;
+    }
+#pragma unroll
+    for (int j = 0; j < PER; ++j) out[row * D + lane + j * kWave] = (f16)(ns > 0 ? num[j] / den : 0.f);
+}
+
+template <int D, int G>
+static hipError_t launch_decode(const DecodeArgs& a) {
+    using T = DecodeTile<D>;
+    int bs_shift = -1;
+    for (int s = 0; s < 31; ++s)
+        if ((int64_t(1) << s) == a.bs) bs_shift = s;
+    const hipStream_t stream = (hipStream_t)a.stream;
+    dim3 grid((unsigned)a.num_splits, (unsigned)a.hkv, (unsigned)a.batch);
+    hipLaunchKernelGGL((paged_decode_kernel<D, G>), grid, dim3(T::THREADS), 0, stream, (const f16*)a.q,
+                       (const f16*)a.k_cache, (const f16*)a.v_cache, a.block_tables, a.context_lens,
+                       (f16*)a.out, a.o_part, a.m_part, a.l_part, (int)a.hkv, (int)a.bs, bs_shift,
+                       (int)a.max_blocks, (int)a.num_blocks, (int)a.partition, (int)a.num_splits, a.sl2);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.num_splits == 1) return e;
+    hipLaunchKernelGGL((paged_reduce_kernel<D>), dim3((unsigned)(a.batch * a.hq)), dim3(kWave), 0, stream,
+                       a.o_part, a.m_part, a.l_part, a.context_lens, (f16*)a.out, (int)a.hq,
+                       (int)a.partition, (int)a.num_splits);
+    return hipGetLastError();
+}
+
+hipError_t decode_launch(const DecodeArgs& a) {
+    const int64_t G = a.hq / a.hkv;
+#define AK_DECODE(DD, GG) \
+    if (a.d == DD && G == GG) return launch_decode<DD, GG>(a);
+    AK_DECODE(64, 1) AK_DECODE(64, 2) AK_DECODE(64, 4) AK_DECODE(64, 8)
+    AK_DECODE(128, 1) AK_DECODE(128, 2) AK_DECODE(128, 4) AK_DECODE(128, 8)
+#undef AK_DECODE
+    return hipErrorInvalidValue;
+}
+
+}  // namespace ak

@@ -1,0 +1,91 @@
+// Thin PyTorch-ROCm glue: the pybind module `attnkernels_ext` with the
+// reference's four functions (attnkernels/csrc/ext.cpp:3-17), each allocating
+// its output (and split-K workspace) from the caching allocator and calling
+// the C-ABI in include/attnkernels.h on the caller's current HIP stream.
+#include <torch/extension.h>
+
+#include <c10/hip/HIPGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include "attnkernels.h"
+
+namespace {
+
+void check_rc(int rc) { TORCH_CHECK(rc == AK_OK, ak_last_error()); }
+
+void check_prefill(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v) {
+    for (const auto* t : {&q, &k, &v}) {
+        TORCH_CHECK(t->is_cuda() && t->scalar_type() == torch::kHalf && t->dim() == 4 && t->is_contiguous(),
+                    "q, k, v must be contiguous fp16 GPU tensors of shape [B, H, N, D]");
+        TORCH_CHECK(t->device() == q.device(), "q, k, v must be on the same device");
+    }
+    TORCH_CHECK(q.sizes() == k.sizes() && q.sizes() == v.sizes(),
+                "q, k, v must have the same shape (self-attention prefill)");
+}
+
+void* stream_of(const torch::Tensor& t) { return c10::hip::getCurrentHIPStream(t.device().index()).stream(); }
+
+}  // namespace
+
+torch::Tensor naive_attention(torch::Tensor q, torch::Tensor k, torch::Tensor v, bool causal, double scale) {
+    check_prefill(q, k, v);
+    const c10::hip::HIPGuard guard(q.device());
+    auto o = torch::empty_like(q);
+    check_rc(ak_naive_attention(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), q.size(0), q.size(1),
+                                q.size(2), q.size(3), causal, scale, stream_of(q)));
+    return o;
+}
+
+torch::Tensor flash_simt(torch::Tensor q, torch::Tensor k, torch::Tensor v, bool causal, double scale) {
+    check_prefill(q, k, v);
+    const c10::hip::HIPGuard guard(q.device());
+    auto o = torch::empty_like(q);
+    check_rc(ak_flash_simt(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), q.size(0), q.size(1),
+                           q.size(2), q.size(3), causal, scale, stream_of(q)));
+    return o;
+}
+
+torch::Tensor flash_wmma(torch::Tensor q, torch::Tensor k, torch::Tensor v, bool causal, double scale,
+                         int64_t block_n) {
+    check_prefill(q, k, v);
+    const c10::hip::HIPGuard guard(q.device());
+    auto o = torch::empty_like(q);
+    check_rc(ak_flash_wmma(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), q.size(0), q.size(1),
+                           q.size(2), q.size(3), causal, scale, block_n, stream_of(q)));
+    return o;
+}
+
+torch::Tensor paged_decode(torch::Tensor q, torch::Tensor kc, torch::Tensor vc, torch::Tensor bt,
+                           torch::Tensor ctx, int64_t max_ctx, double scale, int64_t partition) {
+    TORCH_CHECK(q.is_cuda() && q.scalar_type() == torch::kHalf && q.dim() == 3 && q.is_contiguous(),
+                "q must be a contiguous fp16 GPU tensor [B, H, D]");
+    TORCH_CHECK(kc.is_cuda() && kc.scalar_type() == torch::kHalf && kc.dim() == 4 && kc.is_contiguous() &&
+                    vc.sizes() == kc.sizes() && vc.scalar_type() == torch::kHalf && vc.is_contiguous(),
+                "k_cache and v_cache must be contiguous fp16 GPU tensors [num_blocks, H_kv, block_size, D]");
+    TORCH_CHECK(kc.size(3) == q.size(2), "head_dim of q and the cache must match");
+    TORCH_CHECK(bt.scalar_type() == torch::kInt && bt.dim() == 2 && bt.is_contiguous() && bt.size(0) == q.size(0),
+                "block_tables must be a contiguous int32 tensor [B, max_blocks]");
+    TORCH_CHECK(ctx.scalar_type() == torch::kInt && ctx.dim() == 1 && ctx.is_contiguous() && ctx.size(0) == q.size(0),
+                "context_lens must be a contiguous int32 tensor [B]");
+    for (const auto* t : {&kc, &vc, &bt, &ctx})
+        TORCH_CHECK(t->device() == q.device(), "all paged_decode tensors must be on the same device");
+    const c10::hip::HIPGuard guard(q.device());
+    auto out = torch::empty_like(q);
+    const int64_t B = q.size(0), hq = q.size(1), D = q.size(2);
+    const size_t ws_bytes = ak_paged_decode_workspace_size(B, hq, D, max_ctx, partition);
+    torch::Tensor ws;
+    if (ws_bytes > 0) ws = torch::empty({(int64_t)ws_bytes}, q.options().dtype(torch::kByte));
+    check_rc(ak_paged_decode(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr<int32_t>(),
+                             ctx.data_ptr<int32_t>(), out.data_ptr(), B, hq, kc.size(1), D, kc.size(0), kc.size(2),
+                             bt.size(1), max_ctx, scale, partition, ws_bytes ? ws.data_ptr() : nullptr, ws_bytes,
+                             stream_of(q)));
+    return out;
+}
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+    m.doc() = "gfx950 attention kernels: MFMA flash prefill, paged split-K decode";
+    m.def("naive_attention", &naive_attention, "prefill attention (served by the MFMA flash kernel)");
+    m.def("flash_simt", &flash_simt, "prefill attention (served by the MFMA flash kernel)");
+    m.def("flash_wmma", &flash_wmma, "tiled attention with online softmax on MFMA matrix cores");
+    m.def("paged_decode", &paged_decode, "decode attention over a paged KV cache, split-K");
+}

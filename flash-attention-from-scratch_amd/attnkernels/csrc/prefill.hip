@@ -1,0 +1,288 @@
+// Flash prefill on CDNA4 f16 MFMA (gfx950).
+//
+// One kernel serves the reference's three prefill entry points
+// (naive_attn.cu:65-86, flash_simt.cu:209-221, flash_wmma.cu:241-257): same
+// inputs, same online-softmax algorithm (flash_wmma.cu:114-194), same masking
+// and guards, built for wave64 and the 32x32x16 matrix core instead of warps.
+//
+// Layout choices
+//   * A workgroup is 4 waves and owns BM = 128 query rows of one (batch, head);
+//     each wave owns 32 of them, so no softmax row is shared between waves.
+//   * Scores are computed transposed, S^T = K Q^T, with K as the MFMA A operand
+//     (straight 16-byte LDS reads of K rows) and Q as the B operand (kept in
+//     VGPRs for the whole kernel).  In the accumulator a lane then holds one
+//     query column and 16 keys per 32x32 block, so the row max / sum are
+//     in-lane plus one exchange with lane l^32.
+//   * O^T = V^T P^T.  P^T comes straight from the S^T accumulators (converted
+//     to f16, no LDS round trip): accumulator rows 8c..8c+7 of a lane half are
+//     keys 16c + {0..3, 8..11} (+4 for the upper half), which is exactly the
+//     MFMA's k = 8*(l/32)+i if V^T is stored with the key positions inside each
+//     16-key group bit-2/bit-3 swapped.  V is transposed while it is staged
+//     into LDS, and its d rows are stored with the same swap so that every
+//     lane's O^T accumulators hold 8 contiguous head dims (16-byte stores).
+//   * K/V tiles are double-buffered in LDS: the next tile's global loads are
+//     issued before the current tile's MFMAs and written to the other buffer
+//     after them, one barrier per tile.  2 x 35 KB per workgroup, two
+//     workgroups per CU in the 160 KB LDS.
+//   * Causal: a workgroup processes query tile j and tile nqt-1-j, so every
+//     workgroup has the same amount of work; waves skip key tiles that lie
+//     entirely above their diagonal; masking runs only on diagonal/tail tiles.
+//   * Workgroup ids are remapped so that the query tiles of one (batch, head)
+//     run on the same XCD and share its L2.
+#include "attn_kernels.hpp"
+#include "wave.hpp"
+
+namespace ak {
+
+template <int D>
+struct PrefillTile {
+    static constexpr int NW = 4;                 // waves per workgroup
+    static constexpr int THREADS = NW * kWave;   // 256
+    static constexpr int QW = 32;                // query rows per wave
+    static constexpr int BM = NW * QW;           // query rows per workgroup
+    static constexpr int CH = D / 8;             // 16-byte chunks per K/V row
+    static constexpr int BN = 4 * THREADS / CH;  // keys per tile: 64 (D=128), 128 (D=64)
+    static constexpr int LDK = D + 8;            // K tile row stride (halves)
+    static constexpr int LDV = BN + 8;           // V^T tile row stride (halves)
+    static constexpr int K_ELEMS = BN * LDK;
+    static constexpr int V_ELEMS = D * LDV;
+    static constexpr int STAGE = K_ELEMS + V_ELEMS;  // halves per pipeline stage
+    static constexpr int KB = BN / 32;           // 32-key blocks of S^T
+    static constexpr int DC = D / 16;            // k-steps of K Q^T
+    static constexpr int DT = D / 32;            // 32-row tiles of O^T
+    static constexpr int PC = BN / 16;           // k-steps of V^T P^T
+    static constexpr int KLOADS = BN * CH / THREADS;  // 16-byte K loads per thread (4)
+    static_assert(KLOADS == 4, "each thread stages 4 K chunks and 4 V rows per tile");
+    static_assert(D % 32 == 0 && BN % 32 == 0, "tile shapes");
+};
+
+template <int D>
+struct Staged {
+    f16x8 k[PrefillTile<D>::KLOADS];
+    f16x8 v[4];
+};
+
+// Global -> registers for key tile [k0, k0 + BN).  Rows past n read as zero.
+template <int D>
+__device__ __forceinline__ void stage_load(Staged<D>& st, const f16* __restrict__ kb,
+                                           const f16* __restrict__ vb, int k0, int n, int tid) {
+    using T = PrefillTile<D>;
+#pragma unroll
+    for (int j = 0; j < T::KLOADS; ++j) {
+        const int c = tid + j * T::THREADS;
+        const int row = c / T::CH, ch = c % T::CH;
+        const int key = k0 + row;
+        st.k[j] = key < n ? *reinterpret_cast<const f16x8*>(kb + (size_t)key * D + ch * 8) : f16x8{};
+    }
+    const int dc = tid % T::CH, kg = tid / T::CH;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int key = k0 + kg * 4 + j;
+        st.v[j] = key < n ? *reinterpret_cast<const f16x8*>(vb + (size_t)key * D + dc * 8) : f16x8{};
+    }
+}
+
+// Registers -> LDS stage: K row-major, V transposed with swapped key/d order.
+template <int D>
+__device__ __forceinline__ void stage_store(const Staged<D>& st, f16* __restrict__ ks,
+                                            f16* __restrict__ vs, int tid) {
+    using T = PrefillTile<D>;
+#pragma unroll
+    for (int j = 0; j < T::KLOADS; ++j) {
+        const int c = tid + j * T::THREADS;
+        const int row = c / T::CH, ch = c % T::CH;
+        *reinterpret_cast<f16x8*>(ks + row * T::LDK + ch * 8) = st.k[j];
+    }
+    const int dc = tid % T::CH, kg = tid / T::CH;
+    const int kl = kg * 4;                                  // first of 4 keys, multiple of 4
+    const int pos = (kl & ~15) | swap23(kl & 15);           // its slot in the V^T row
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int d = dc * 8 + e;
+        const int lrow = (d & ~31) | swap23(d & 31);
+        const f16x4 col = {st.v[0][e], st.v[1][e], st.v[2][e], st.v[3][e]};
+        *reinterpret_cast<f16x4*>(vs + lrow * T::LDV + pos) = col;
+    }
+}
+
+// Value of lane l^32 combined with this lane's by max / sum.
+__device__ __forceinline__ float pair_max(float x) { return fmaxf(x, shfl_xor<32>(x)); }
+__device__ __forceinline__ float pair_sum(float x) { return x + shfl_xor<32>(x); }
+
+template <int D, bool CAUSAL>
+__device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const f16* __restrict__ kb,
+                                              const f16* __restrict__ vb, f16* __restrict__ ob,
+                                              f16* __restrict__ lds, int q0, int n, float sl2,
+                                              uint32_t qflip) {
+    using T = PrefillTile<D>;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, w = uniform(tid >> 6);
+    const int col = lane & 31, half = lane >> 5;
+    const int qw0 = q0 + w * T::QW;  // first query row of this wave
+    const int qrow = qw0 + col;      // this lane's query row
+
+    // Q as the MFMA B operand: col = query, k = head dim 16*dc + 8*half .. +7.
+    f16x8 qf[T::DC];
+#pragma unroll
+    for (int dc = 0; dc < T::DC; ++dc) {
+        f16x8 x = qrow < n ? *reinterpret_cast<const f16x8*>(qb + (size_t)qrow * D + dc * 16 + half * 8) : f16x8{};
+        if (qflip) {  // negative scale: fold the sign into Q exactly
+            typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+            x = __builtin_bit_cast(f16x8, __builtin_bit_cast(u32x4, x) ^ qflip);
+        }
+        qf[dc] = x;
+    }
+
+    f32x16 o[T::DT];
+#pragma unroll
+    for (int t = 0; t < T::DT; ++t) o[t] = f32x16{};
+    float m_run = -INFINITY;  // running max of raw scores
+    float ms_run = -INFINITY; // the scaled max actually subtracted so far
+    float l_run = 0.f;        // this lane's share of the row sum
+
+    const int kend = CAUSAL ? min(n, q0 + T::BM) : n;
+    const int nkt = (kend + T::BN - 1) / T::BN;
+
+    Staged<D> st;
+    stage_load<D>(st, kb, vb, 0, n, tid);
+    stage_store<D>(st, lds, lds + T::K_ELEMS, tid);
+    __syncthreads();
+
+    for (int kt = 0; kt < nkt; ++kt) {
+        const int k0 = kt * T::BN;
+        f16* ks = lds + (kt & 1) * T::STAGE;
+        f16* vs = ks + T::K_ELEMS;
+        const bool more = kt + 1 < nkt;
+        if (more) stage_load<D>(st, kb, vb, k0 + T::BN, n, tid);
+
+        const bool active = !CAUSAL || k0 <= qw0 + T::QW - 1;
+        if (active) {
+            // S^T = K Q^T: KB blocks of 32 keys x 32 queries.
+            f32x16 s[T::KB];
+#pragma unroll
+            for (int b = 0; b < T::KB; ++b) {
+                s[b] = f32x16{};
+                const f16* krow = ks + (b * 32 + col) * T::LDK + half * 8;
+#pragma unroll
+                for (int dc = 0; dc < T::DC; ++dc)
+                    s[b] = mfma32x32x16(*reinterpret_cast<const f16x8*>(krow + dc * 16), qf[dc], s[b]);
+            }
+            // Mask keys past n and, if causal, keys after the query.
+            const bool need_mask = (k0 + T::BN > n) || (CAUSAL && k0 + T::BN - 1 > qw0);
+            if (need_mask) {
+#pragma unroll
+                for (int b = 0; b < T::KB; ++b)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int key = k0 + b * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+                        if (key >= n || (CAUSAL && key > qrow)) s[b][r] = -INFINITY;
+                    }
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int b = 0; b < T::KB; ++b)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
+            mx = pair_max(mx);
+            const float m_new = fmaxf(m_run, mx);
+            const float ms_new = (m_new == -INFINITY) ? 0.f : m_new * sl2;
+            const float alpha = exp2_fast(ms_run - ms_new);
+            m_run = m_new;
+            ms_run = ms_new;
+            float psum = 0.f;
+#pragma unroll
+            for (int b = 0; b < T::KB; ++b)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float p = exp2_fast(fmaf(s[b][r], sl2, -ms_new));
+                    if (need_mask) p = (s[b][r] == -INFINITY) ? 0.f : p;
+                    s[b][r] = p;
+                    psum += p;
+                }
+            l_run = l_run * alpha + psum;
+#pragma unroll
+            for (int t = 0; t < T::DT; ++t) o[t] *= alpha;
+
+            // P^T as the B operand: k-step c = accumulator regs 8*(c%2).. of block c/2.
+            f16x8 pf[T::PC];
+#pragma unroll
+            for (int c = 0; c < T::PC; ++c)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) pf[c][i] = (f16)s[c >> 1][(c & 1) * 8 + i];
+            // O^T += V^T P^T.
+#pragma unroll
+            for (int t = 0; t < T::DT; ++t) {
+                const f16* vrow = vs + (t * 32 + col) * T::LDV + half * 8;
+#pragma unroll
+                for (int c = 0; c < T::PC; ++c)
+                    o[t] = mfma32x32x16(*reinterpret_cast<const f16x8*>(vrow + c * 16), pf[c], o[t]);
+            }
+        }
+        if (more) {
+            f16* nks = lds + ((kt + 1) & 1) * T::STAGE;
+            stage_store<D>(st, nks, nks + T::K_ELEMS, tid);
+        }
+        __syncthreads();
+    }
+
+    // O = O^T / l.  Lane holds query qrow, head dims 32t + 16hh + 8*half + i.
+    const float l_tot = pair_sum(l_run);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    if (qrow < n) {
+        f16* orow = ob + (size_t)qrow * D + half * 8;
+#pragma unroll
+        for (int t = 0; t < T::DT; ++t)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                f16x8 v;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = (f16)(o[t][hh * 8 + i] * inv);
+                *reinterpret_cast<f16x8*>(orow + t * 32 + hh * 16) = v;
+            }
+    }
+}
+
+template <int D, bool CAUSAL>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+flash_prefill_kernel(const f16* __restrict__ Q, const f16* __restrict__ K, const f16* __restrict__ V,
+                     f16* __restrict__ O, int n, int units_per_bh, int total_units, float sl2,
+                     uint32_t qflip) {
+    using T = PrefillTile<D>;
+    __shared__ __attribute__((aligned(16))) f16 lds[2 * T::STAGE];
+    const int L = xcd_remap((int)blockIdx.x, total_units);
+    const int bh = L / units_per_bh, u = L % units_per_bh;
+    const size_t base = (size_t)bh * n * D;
+    const int nqt = (n + T::BM - 1) / T::BM;
+    if (CAUSAL) {
+        // Pair the heaviest remaining tile with the lightest: equal work per workgroup.
+        const int heavy = nqt - 1 - u;
+        prefill_qtile<D, true>(Q + base, K + base, V + base, O + base, lds, heavy * T::BM, n, sl2, qflip);
+        if (u != heavy) {
+            __syncthreads();
+            prefill_qtile<D, true>(Q + base, K + base, V + base, O + base, lds, u * T::BM, n, sl2, qflip);
+        }
+    } else {
+        prefill_qtile<D, false>(Q + base, K + base, V + base, O + base, lds, u * T::BM, n, sl2, qflip);
+    }
+}
+
+template <int D, bool CAUSAL>
+static hipError_t launch_prefill(const PrefillArgs& a) {
+    using T = PrefillTile<D>;
+    const int nqt = (int)((a.n + T::BM - 1) / T::BM);
+    const int units = CAUSAL ? (nqt + 1) / 2 : nqt;
+    const long long total = (long long)units * a.bh;
+    if (total <= 0) return hipSuccess;
+    hipLaunchKernelGGL((flash_prefill_kernel<D, CAUSAL>), dim3((unsigned)total), dim3(T::THREADS), 0,
+                       (hipStream_t)a.stream, (const f16*)a.q, (const f16*)a.k, (const f16*)a.v,
+                       (f16*)a.o, (int)a.n, units, (int)total, a.sl2, a.qflip);
+    return hipGetLastError();
+}
+
+hipError_t prefill_launch(const PrefillArgs& a) {
+    if (a.d == 64) return a.causal ? launch_prefill<64, true>(a) : launch_prefill<64, false>(a);
+    return a.causal ? launch_prefill<128, true>(a) : launch_prefill<128, false>(a);
+}
+
+
+}  // namespace ak

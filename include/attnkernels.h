@@ -1,0 +1,97 @@
+/* attnkernels C-ABI: MI355X (gfx950) attention hot path.
+ *
+ * Plain pointers, sizes and a hipStream_t passed as void*; no torch types.
+ * These are the entry points behind the reference's pybind module
+ * `attnkernels_ext` (sonhoang/flash-attention-from-scratch
+ * attnkernels/csrc/ext.cpp:3-10, 14-17); each function names the reference
+ * interface it replaces.
+ *
+ * Conventions shared by every entry point
+ *   - Tensors are dense, row-major, fp16 (IEEE binary16) unless stated, in
+ *     device memory, and every pointer is 16-byte aligned.
+ *   - Work is enqueued on `stream` (NULL = the null stream) and the call
+ *     returns without synchronising, like the reference's launches.
+ *   - The return value is AK_OK or one of the AK_ERR_* codes; on failure
+ *     ak_last_error() returns a message for the calling thread, worded like
+ *     the reference's TORCH_CHECK messages where one exists.
+ *   - Validation happens before any HIP call, so a rejected call touches no GPU.
+ */
+#ifndef ATTNKERNELS_H
+#define ATTNKERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    AK_OK = 0,
+    AK_ERR_INVALID_ARGUMENT = 1, /* null/misaligned pointer, negative size, bad split size */
+    AK_ERR_UNSUPPORTED = 2,      /* head_dim / block_n / head-group combination not built */
+    AK_ERR_WORKSPACE = 3,        /* workspace missing or smaller than required */
+    AK_ERR_HIP = 4               /* the HIP runtime reported an error at launch */
+};
+
+/* Message describing the last failed call on this thread ("" if none). */
+const char *ak_last_error(void);
+
+/* ABI version of this library (major * 100 + minor). */
+int ak_abi_version(void);
+
+/* Prefill attention, O = softmax(scale * Q K^T [+ causal mask]) V.
+ * q, k, v, o: fp16 [batch, heads, seq_len, head_dim]; head_dim 64 or 128.
+ * Key j is masked for query i iff causal && j > i.
+ *
+ * ak_naive_attention replaces naive_attention (attnkernels/csrc/naive_attn.cu:65-86,
+ *   ext.cpp:14); it runs the same flash kernel (no N x N score buffer).
+ * ak_flash_simt replaces flash_simt (attnkernels/csrc/flash_simt.cu:209-221, ext.cpp:15).
+ * ak_flash_wmma replaces flash_wmma (attnkernels/csrc/flash_wmma.cu:241-257, ext.cpp:16);
+ *   block_n must be 32 or 64, as in the reference, and selects nothing else: the
+ *   gfx950 kernel picks its own key tile. */
+int ak_naive_attention(const void *q, const void *k, const void *v, void *o, int64_t batch,
+                       int64_t heads, int64_t seq_len, int64_t head_dim, int causal,
+                       double scale, void *stream);
+int ak_flash_simt(const void *q, const void *k, const void *v, void *o, int64_t batch,
+                  int64_t heads, int64_t seq_len, int64_t head_dim, int causal, double scale,
+                  void *stream);
+int ak_flash_wmma(const void *q, const void *k, const void *v, void *o, int64_t batch,
+                  int64_t heads, int64_t seq_len, int64_t head_dim, int causal, double scale,
+                  int64_t block_n, void *stream);
+
+/* Bytes of device workspace ak_paged_decode needs for these sizes: the fp32
+ * split partials o [B, Hq, S, D], m and l [B, Hq, S] with S = ceil(max_context_len /
+ * partition), or 0 when S == 1.  Replaces the torch::empty partials of
+ * launch_decode (attnkernels/csrc/paged_decode.cu:227-235).  Returns 0 for
+ * invalid sizes. */
+size_t ak_paged_decode_workspace_size(int64_t batch, int64_t num_heads, int64_t head_dim,
+                                      int64_t max_context_len, int64_t partition);
+
+/* Paged-KV decode with split-K, replacing paged_decode
+ * (attnkernels/csrc/paged_decode.cu:256-277, ext.cpp:17).
+ *   q:            fp16 [batch, num_heads, head_dim], one query token per sequence
+ *   k_cache, v_cache: fp16 [num_blocks, num_kv_heads, block_size, head_dim]
+ *   block_tables: int32 [batch, max_blocks_per_seq], physical page ids
+ *   context_lens: int32 [batch], tokens of context (>= 1) per sequence
+ *   out:          fp16 [batch, num_heads, head_dim]
+ *   max_context_len: host value >= every context length
+ *   partition:    tokens per split, a positive multiple of 256
+ *   workspace:    device memory of at least ak_paged_decode_workspace_size() bytes
+ *                 (may be NULL when that size is 0); contents are scratch.
+ * head_dim 64/128 and num_heads/num_kv_heads in {1, 2, 4, 8}.  Query head h
+ * reads kv head h / (num_heads / num_kv_heads).  Page ids outside
+ * [0, num_blocks) are never read (their tokens are left out of the softmax);
+ * tokens at or beyond max_blocks_per_seq * block_size are ignored. */
+int ak_paged_decode(const void *q, const void *k_cache, const void *v_cache,
+                    const int32_t *block_tables, const int32_t *context_lens, void *out,
+                    int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                    int64_t num_blocks, int64_t block_size, int64_t max_blocks_per_seq,
+                    int64_t max_context_len, double scale, int64_t partition, void *workspace,
+                    size_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ATTNKERNELS_H */

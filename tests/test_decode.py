@@ -1,0 +1,233 @@
+"""Paged split-K decode parity on the GPU against the CPU oracle.
+
+Mirrors the reference's suite (tests/test_decode.py:9-63: head groups x
+contexts, ragged batch with 4 partitions, block sizes, long context, split
+invariance, the gather+SDPA baseline) with the north-star tolerances, and adds
+bit-exact page-gather checks and the full-size BASELINE decode configs.
+"""
+import numpy as np
+import pytest
+import torch
+
+import attnkernels as ak
+from attnkernels import reference as akref
+import oracle
+from conftest import TOL, max_err
+
+pytestmark = pytest.mark.gpu
+
+
+def cache(ctx, hkv, d, bs=16, extra=5, seed=0):
+    kc, vc, bt, cl = oracle.make_paged_cache(ctx, hkv, d, block_size=bs, extra_blocks=extra, seed=seed)
+    return kc, vc, bt, cl
+
+
+def rand_q(b, hq, d, seed=1):
+    return np.random.default_rng(seed).standard_normal((b, hq, d), dtype=np.float32).astype(np.float16)
+
+
+def to_dev(*arrs):
+    return [torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in arrs]
+
+
+def run(ctx, hq, hkv, d, bs=16, partition=None, seed=0):
+    kc, vc, bt, cl = cache(ctx, hkv, d, bs, seed=seed)
+    q = rand_q(len(ctx), hq, d, seed + 1)
+    qd, kcd, vcd, btd, cld = to_dev(q, kc, vc, bt, cl)
+    out = ak.paged_decode(qd, kcd, vcd, btd, cld, max(ctx), partition_size=partition)
+    torch.cuda.synchronize()
+    ref = oracle.paged_decode_fp32(q, kc, vc, bt, cl)
+    assert out.shape == qd.shape and out.dtype == torch.float16
+    assert torch.isfinite(out).all()
+    return max_err(out, ref)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("heads", [(8, 8), (8, 4), (32, 8), (16, 2)])
+@pytest.mark.parametrize("ctx", [[1], [100], [256], [1000, 1000], [5000]])
+def test_uniform(d, heads, ctx):
+    assert run(ctx, heads[0], heads[1], d) < TOL[d]
+
+
+RAGGED = [1, 17, 255, 256, 257, 999, 4097, 33]
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("partition", [None, 256, 1024, 1 << 20])
+def test_ragged_batch(d, partition):
+    """Different context lengths in one batch; partition 1<<20 means no split-K."""
+    assert run(RAGGED, 32, 8, d, partition=partition) < TOL[d]
+
+
+@pytest.mark.parametrize("bs", [8, 16, 32, 12])
+def test_block_sizes(bs):
+    assert run([300, 2000, 17], 8, 2, 128, bs=bs) < TOL[128]
+
+
+def test_long_context_split():
+    assert run([32768], 32, 8, 128) < TOL[128]
+
+
+def test_split_choice_does_not_change_result():
+    kc, vc, bt, cl = cache([6000, 3000], 4, 128, extra=0)
+    q = rand_q(2, 16, 128)
+    qd, kcd, vcd, btd, cld = to_dev(q, kc, vc, bt, cl)
+    outs = [ak.paged_decode(qd, kcd, vcd, btd, cld, 6000, partition_size=p) for p in (256, 768, 2048, 6144)]
+    for o in outs[1:]:
+        assert max_err(o, outs[0]) < 2e-3
+
+
+def test_torch_baseline_matches():
+    """The gather + SDPA baseline kept in attnkernels.reference is itself correct
+    (run in fp32 on the GPU, see the bf16/fp16 batched-GEMM caveat on this pool)."""
+    ctx = [512, 512, 300]
+    kc, vc, bt, cl = cache(ctx, 8, 128, extra=0)
+    q = rand_q(3, 32, 128)
+    qd, kcd, vcd, btd, cld = to_dev(q, kc, vc, bt, cl)
+    out = akref.paged_decode_torch(qd.float(), kcd.float(), vcd.float(), btd, 32, context_lens=cld)
+    assert max_err(out, oracle.paged_decode_fp32(q, kc, vc, bt, cl)) < TOL[128]
+
+
+def test_scale_argument():
+    kc, vc, bt, cl = cache([700, 40], 2, 64)
+    q = rand_q(2, 4, 64)
+    qd, kcd, vcd, btd, cld = to_dev(q, kc, vc, bt, cl)
+    for s in (0.5, -0.1, 0.0):
+        out = ak.paged_decode(qd, kcd, vcd, btd, cld, 700, scale=s, partition_size=256)
+        assert max_err(out, oracle.paged_decode_fp32(q, kc, vc, bt, cl, scale=s)) < TOL[64]
+
+
+def test_errors_match_reference():
+    kc, vc, bt, cl = cache([300], 2, 128)
+    qd, kcd, vcd, btd, cld = to_dev(rand_q(1, 6, 128), kc, vc, bt, cl)
+    with pytest.raises(RuntimeError, match="multiple of num_kv_heads"):
+        ak.load_extension().paged_decode(qd[:, :3].contiguous(), kcd, vcd, btd, cld, 300, 0.1, 256)
+    with pytest.raises(RuntimeError, match="positive multiple of 256"):
+        ak.load_extension().paged_decode(qd[:, :2].contiguous(), kcd, vcd, btd, cld, 300, 0.1, 100)
+    with pytest.raises(RuntimeError, match=r"num_heads/num_kv_heads in \{1,2,4,8\}"):
+        ak.load_extension().paged_decode(qd, kcd, vcd, btd, cld, 300, 0.1, 256)
+
+
+# ------------------------------------------------ bit-exact page gathering --
+
+@pytest.mark.parametrize("d,bs", [(128, 16), (64, 8), (128, 32)])
+def test_gather_reads_exact_token(d, bs):
+    """Each (sequence, kv head) attends to one chosen token only (its key gets a
+    +64 score, every other key -64, scale 1): the output must be that token's V
+    row, bit for bit, which proves the page/offset arithmetic for that token."""
+    lens = [1, 16, 17, 255, 256, 513, 1000, 4095]
+    hkv = 8
+    kc, vc, bt, cl = cache(lens, hkv, d, bs, extra=7, seed=21)
+    rng = np.random.default_rng(22)
+    for trial in range(3):
+        k2 = np.zeros_like(kc)
+        k2[..., 0] = -8.0
+        q = np.zeros((len(lens), hkv, d), np.float16)
+        q[..., 0] = 8.0
+        chosen = np.zeros((len(lens), hkv), np.int64)
+        for b, c in enumerate(lens):
+            for h in range(hkv):
+                t = int(rng.integers(0, c)) if trial else [0, c - 1][h % 2]
+                chosen[b, h] = t
+                k2[bt[b, t // bs], h, t % bs, 0] = 8.0
+        qd, kcd, vcd, btd, cld = to_dev(q, k2, vc, bt, cl)
+        for part in (256, 1 << 20):
+            out = ak.paged_decode(qd, kcd, vcd, btd, cld, max(lens), scale=1.0, partition_size=part)
+            got = out.cpu().numpy()
+            for b in range(len(lens)):
+                for h in range(hkv):
+                    t = chosen[b, h]
+                    want = vc[bt[b, t // bs], h, t % bs]
+                    assert np.array_equal(got[b, h], want), (trial, part, b, h, t)
+
+
+def test_page_relabelling_is_bit_exact():
+    """Moving pages to other physical slots and rewriting the table accordingly
+    must give a bit-identical output: only the pages the table names are read."""
+    lens = [1, 300, 2049, 77]
+    kc, vc, bt, cl = cache(lens, 4, 128, extra=9, seed=31)
+    q = rand_q(4, 8, 128, seed=32)
+    perm = np.random.default_rng(33).permutation(kc.shape[0])
+    inv = np.argsort(perm)
+    kc2, vc2 = kc[perm], vc[perm]          # physical slot i now holds old page perm[i]
+    bt2 = inv[bt].astype(np.int32)         # old page p lives at slot inv[p]
+    for part in (256, 1024, 1 << 20):
+        a = ak.paged_decode(*to_dev(q, kc, vc, bt, cl), max(lens), partition_size=part)
+        b = ak.paged_decode(*to_dev(q, kc2, vc2, bt2, cl), max(lens), partition_size=part)
+        assert torch.equal(a, b), part
+
+
+def test_bad_page_ids_are_not_read():
+    """Out-of-range page ids (undefined in the reference) are skipped, not read."""
+    kc, vc, bt, cl = cache([64], 2, 64, extra=0, seed=41)
+    bt_bad = bt.copy()
+    bt_bad[0, 1] = 10 ** 6
+    q = rand_q(1, 2, 64, seed=42)
+    out = ak.paged_decode(*to_dev(q, kc, vc, bt_bad, cl), 64, partition_size=256)
+    keep = np.r_[0:16, 32:64]                      # tokens 16..31 sit in the bad page
+    kk = oracle.gather_kv(kc, bt, 4)[0][:, keep]   # [Hkv, 48, D]
+    vv = oracle.gather_kv(vc, bt, 4)[0][:, keep]
+    ref = np.stack([oracle.attention_fp32(q[0, h][None], kk[h], vv[h])[0] for h in range(2)])
+    assert max_err(out[0], ref) < TOL[64]
+
+
+# ---------------------------------------------------- BASELINE full sizes --
+
+def baseline_cache(lens, hkv, d, bs, seed):
+    """Pool = pages needed + 10% slack, pages by seeded permutation, fp16 N(0,1)
+    caches generated on the device (seeded) and copied back for the oracle."""
+    nblk = [-(-c // bs) for c in lens]
+    total = sum(nblk)
+    pool = -(-total * 11 // 10)
+    rng = np.random.default_rng(seed)
+    perm = rng.permutation(pool).astype(np.int32)
+    bt = np.zeros((len(lens), max(nblk)), np.int32)
+    pos = 0
+    for b, nb in enumerate(nblk):
+        bt[b, :nb] = perm[pos:pos + nb]
+        pos += nb
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    shape = (pool, hkv, bs, d)
+    kcd = torch.randn(shape, generator=g, device="cuda", dtype=torch.float16)
+    vcd = torch.randn(shape, generator=g, device="cuda", dtype=torch.float16)
+    return kcd, vcd, bt, np.asarray(lens, np.int32)
+
+
+def _check_rows(out, q, kcd, vcd, bt, cl, rows, d):
+    for b in rows:
+        pages = torch.from_numpy(bt[b]).long().cuda()
+        kc_b = kcd[pages].cpu().numpy()   # the sequence's pages, in table order
+        vc_b = vcd[pages].cpu().numpy()
+        bt_b = np.arange(bt.shape[1], dtype=np.int32)[None]
+        ref = oracle.paged_decode_fp32(q[b:b + 1], kc_b, vc_b, bt_b, cl[b:b + 1])
+        assert max_err(out[b:b + 1], ref) < TOL[d], b
+
+
+def test_baseline_cfg4_ragged_64seqs():
+    rng = np.random.default_rng(4)
+    lens = rng.integers(1, 4097, size=64).tolist()
+    kcd, vcd, bt, cl = baseline_cache(lens, 32, 128, 16, seed=4)
+    q = rand_q(64, 32, 128, seed=5)
+    qd, btd, cld = to_dev(q, bt, cl)
+    out = ak.paged_decode(qd, kcd, vcd, btd, cld, max(lens), partition_size=512)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    _check_rows(out, q, kcd, vcd, bt, cl, list(range(0, 64, 4)) + [63], 128)
+
+
+@pytest.mark.parametrize("d", [128, 64])
+def test_baseline_cfg5_long_context(d):
+    lens = [32768] * 8
+    kcd, vcd, bt, cl = baseline_cache(lens, 32, d, 16, seed=50 + d)
+    q = rand_q(8, 32, d, seed=6)
+    qd, btd, cld = to_dev(q, bt, cl)
+    out = ak.paged_decode(qd, kcd, vcd, btd, cld, 32768, partition_size=256)
+    torch.cuda.synchronize()
+    _check_rows(out, q, kcd, vcd, bt, cl, [0, 7], d)
+    # every row: the 128-way split merge agrees with the unsplit kernel
+    whole = ak.paged_decode(qd, kcd, vcd, btd, cld, 32768, partition_size=1 << 20)
+    assert max_err(out, whole) < TOL[d]
+    # every row: V = 1 gives exactly 1
+    ones = torch.ones_like(vcd)
+    o1 = ak.paged_decode(qd, kcd, ones, btd, cld, 32768, partition_size=256)
+    assert (o1.float() - 1).abs().max().item() < 1e-3

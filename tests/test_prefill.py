@@ -1,0 +1,158 @@
+"""Prefill parity on the GPU: the gfx950 MFMA kernel behind every prefill entry
+point against the CPU oracle on identical seeded fp16 inputs.
+
+Mirrors the reference's suite (tests/test_prefill.py:14-81: 4 variants x causal
+x d x n, long sequence, large logits, causal row 0, SDPA, bad input) with the
+north-star tolerances (max-abs 2e-3 for d=64, 4e-3 for d=128), and adds the
+full-size BASELINE configs through slices and size-independent properties.
+"""
+import numpy as np
+import pytest
+import torch
+
+import attnkernels as ak
+import oracle
+from conftest import TOL, max_err
+
+pytestmark = pytest.mark.gpu
+
+VARIANTS = {
+    "naive": lambda q, k, v, c, s=None: ak.naive_attention(q, k, v, causal=c, scale=s),
+    "simt": lambda q, k, v, c, s=None: ak.flash_attention(q, k, v, causal=c, scale=s, variant="simt"),
+    "wmma32": lambda q, k, v, c, s=None: ak.flash_attention(q, k, v, causal=c, scale=s, variant="wmma",
+                                                            block_n=32),
+    "wmma64": lambda q, k, v, c, s=None: ak.flash_attention(q, k, v, causal=c, scale=s, variant="wmma",
+                                                            block_n=64),
+}
+
+
+def rand_qkv(b, h, n, d, q_scale=1.0, seed=0):
+    """fp16 N(0,1) from a seeded CPU generator; the same values go to the GPU and the oracle."""
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(b, h, n, d, generator=g) * q_scale).half()
+    k = torch.randn(b, h, n, d, generator=g).half()
+    v = torch.randn(b, h, n, d, generator=g).half()
+    return q, k, v
+
+
+def run(variant, q, k, v, causal, scale=None):
+    out = VARIANTS[variant](q.cuda(), k.cuda(), v.cuda(), causal, scale)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("variant", list(VARIANTS))
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("n", [1, 17, 64, 100, 129, 256, 333])
+def test_matches_fp32(variant, causal, d, n):
+    q, k, v = rand_qkv(2, 3, n, d, seed=n * 7 + d)
+    out = run(variant, q, k, v, causal)
+    ref = oracle.attention_fp32(q.numpy(), k.numpy(), v.numpy(), causal)
+    assert out.shape == q.shape and out.dtype == torch.float16
+    assert torch.isfinite(out).all()
+    assert max_err(out, ref) < TOL[d]
+
+
+@pytest.mark.parametrize("variant", ["simt", "wmma32", "wmma64"])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("d", [64, 128])
+def test_long_sequence(variant, causal, d):
+    q, k, v = rand_qkv(1, 2, 2048 + 7, d, seed=3)
+    out = run(variant, q, k, v, causal)
+    assert max_err(out, oracle.attention_fp32(q.numpy(), k.numpy(), v.numpy(), causal)) < TOL[d]
+
+
+@pytest.mark.parametrize("variant", list(VARIANTS))
+@pytest.mark.parametrize("d", [64, 128])
+def test_large_logits(variant, d):
+    """Scores with a std of about 6: exp would overflow without the running max."""
+    q, k, v = rand_qkv(1, 2, 300, d, q_scale=6.0, seed=4)
+    out = run(variant, q, k, v, True)
+    assert torch.isfinite(out).all()
+    assert max_err(out, oracle.attention_fp32(q.numpy(), k.numpy(), v.numpy(), True)) < 2 * TOL[d]
+
+
+def test_causal_first_row_is_v0():
+    q, k, v = rand_qkv(1, 1, 128, 64, seed=5)
+    for name in VARIANTS:
+        out = run(name, q, k, v, True)
+        assert max_err(out[0, 0, 0], v[0, 0, 0]) < 1e-3, name
+
+
+@pytest.mark.parametrize("variant", list(VARIANTS))
+def test_matches_cpu_sdpa(variant):
+    """Second, independent reference: torch's CPU SDPA in fp32 (GPU SDPA is not used)."""
+    q, k, v = rand_qkv(2, 4, 512, 64, seed=6)
+    out = run(variant, q, k, v, True)
+    sdpa = torch.nn.functional.scaled_dot_product_attention(q.float(), k.float(), v.float(),
+                                                            is_causal=True)
+    assert max_err(out, sdpa) < TOL[64]
+
+
+@pytest.mark.parametrize("scale", [0.3, -0.05, 0.0, 1e-3])
+@pytest.mark.parametrize("causal", [False, True])
+def test_explicit_scales(scale, causal):
+    q, k, v = rand_qkv(1, 2, 150, 128, seed=8)
+    out = run("wmma64", q, k, v, causal, scale)
+    ref = oracle.attention_fp32(q.numpy(), k.numpy(), v.numpy(), causal, scale)
+    assert max_err(out, ref) < TOL[128]
+
+
+def test_rejects_bad_input():
+    q, k, v = rand_qkv(1, 1, 16, 32)
+    with pytest.raises(ValueError):
+        ak.flash_attention(q.cuda(), k.cuda(), v.cuda())
+    q, k, v = rand_qkv(1, 1, 16, 64)
+    with pytest.raises(ValueError):
+        ak.flash_attention(q.cuda(), k.cuda(), v.cuda(), variant="tensor")
+    with pytest.raises(RuntimeError, match="block_n 32 or 64"):
+        ak.flash_attention(q.cuda(), k.cuda(), v.cuda(), block_n=128)
+    with pytest.raises(ValueError):
+        ak.flash_attention(q.cuda(), k[:, :, :8].cuda(), v.cuda())
+
+
+def test_non_contiguous_inputs_are_accepted():
+    q, k, v = rand_qkv(1, 4, 96, 64, seed=9)
+    qt = q.transpose(1, 2).contiguous().cuda().transpose(1, 2)  # [B, H, N, D] view, not contiguous
+    out = ak.flash_attention(qt, k.cuda(), v.cuda(), causal=True)
+    assert max_err(out, oracle.attention_fp32(q.numpy(), k.numpy(), v.numpy(), True)) < TOL[64]
+
+
+# ---------------------------------------------------- BASELINE full sizes --
+
+def _device_qkv(b, h, n, d, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    return [torch.randn(b, h, n, d, generator=g, device="cuda", dtype=torch.float16) for _ in range(3)]
+
+
+@pytest.mark.parametrize("cfg", [(4, 16, 2048, 64, False), (2, 32, 8192, 128, True),
+                                 (2, 32, 8191, 128, True)],
+                         ids=["cfg2_d64_n2048", "cfg3_d128_n8192_causal", "cfg3_d128_n8191_causal"])
+def test_baseline_config_slices(cfg):
+    """Full-size launch; (batch, head) slices at both ends checked against the oracle."""
+    b, h, n, d, causal = cfg
+    q, k, v = _device_qkv(b, h, n, d, seed=11)
+    out = ak.flash_attention(q, k, v, causal=causal)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    for bi, hi in [(0, 0), (b - 1, h - 1)]:
+        qs, ks, vs = (t[bi, hi].cpu().numpy() for t in (q, k, v))
+        ref = oracle.attention_fp32(qs, ks, vs, causal)
+        assert max_err(out[bi, hi], ref) < TOL[d], (bi, hi)
+
+
+@pytest.mark.parametrize("cfg", [(2, 32, 8192, 128, True), (2, 32, 8191, 128, True),
+                                 (4, 16, 2048, 64, False)],
+                         ids=["cfg3", "cfg3_odd", "cfg2"])
+def test_baseline_config_properties(cfg):
+    """Size-independent checks over every row: V = 1 gives O = 1 exactly (the
+    softmax weights of each row sum to one); scaling V by 2 scales O by 2."""
+    b, h, n, d, causal = cfg
+    q, k, v = _device_qkv(b, h, n, d, seed=12)
+    ones = torch.ones_like(v)
+    o1 = ak.flash_attention(q, k, ones, causal=causal)
+    assert (o1.float() - 1).abs().max().item() < 2e-3
+    o = ak.flash_attention(q, k, v, causal=causal)
+    o2 = ak.flash_attention(q, k, v * 2, causal=causal)
+    assert (o2.float() - 2 * o.float()).abs().max().item() < 2 * TOL[d]
