@@ -4,8 +4,10 @@
 // the C-ABI in include/attnkernels.h on the caller's current HIP stream.
 #include <torch/extension.h>
 
-#include <c10/hip/HIPGuard.h>
-#include <c10/hip/HIPStream.h>
+// PyTorch-ROCm reports GPU tensors with device type "cuda"; these are its
+// guard and stream accessors for that device type.
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 
 #include "attnkernels.h"
 
@@ -23,13 +25,15 @@ void check_prefill(const torch::Tensor& q, const torch::Tensor& k, const torch::
                 "q, k, v must have the same shape (self-attention prefill)");
 }
 
-void* stream_of(const torch::Tensor& t) { return c10::hip::getCurrentHIPStream(t.device().index()).stream(); }
+void* stream_of(const torch::Tensor& t) {
+    return at::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.device().index()).stream();
+}
 
 }  // namespace
 
 torch::Tensor naive_attention(torch::Tensor q, torch::Tensor k, torch::Tensor v, bool causal, double scale) {
     check_prefill(q, k, v);
-    const c10::hip::HIPGuard guard(q.device());
+    const at::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     auto o = torch::empty_like(q);
     check_rc(ak_naive_attention(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), q.size(0), q.size(1),
                                 q.size(2), q.size(3), causal, scale, stream_of(q)));
@@ -38,7 +42,7 @@ torch::Tensor naive_attention(torch::Tensor q, torch::Tensor k, torch::Tensor v,
 
 torch::Tensor flash_simt(torch::Tensor q, torch::Tensor k, torch::Tensor v, bool causal, double scale) {
     check_prefill(q, k, v);
-    const c10::hip::HIPGuard guard(q.device());
+    const at::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     auto o = torch::empty_like(q);
     check_rc(ak_flash_simt(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), q.size(0), q.size(1),
                            q.size(2), q.size(3), causal, scale, stream_of(q)));
@@ -48,7 +52,7 @@ torch::Tensor flash_simt(torch::Tensor q, torch::Tensor k, torch::Tensor v, bool
 torch::Tensor flash_wmma(torch::Tensor q, torch::Tensor k, torch::Tensor v, bool causal, double scale,
                          int64_t block_n) {
     check_prefill(q, k, v);
-    const c10::hip::HIPGuard guard(q.device());
+    const at::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     auto o = torch::empty_like(q);
     check_rc(ak_flash_wmma(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), q.size(0), q.size(1),
                            q.size(2), q.size(3), causal, scale, block_n, stream_of(q)));
@@ -69,7 +73,7 @@ torch::Tensor paged_decode(torch::Tensor q, torch::Tensor kc, torch::Tensor vc, 
                 "context_lens must be a contiguous int32 tensor [B]");
     for (const auto* t : {&kc, &vc, &bt, &ctx})
         TORCH_CHECK(t->device() == q.device(), "all paged_decode tensors must be on the same device");
-    const c10::hip::HIPGuard guard(q.device());
+    const at::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     auto out = torch::empty_like(q);
     const int64_t B = q.size(0), hq = q.size(1), D = q.size(2);
     const size_t ws_bytes = ak_paged_decode_workspace_size(B, hq, D, max_ctx, partition);
