@@ -176,6 +176,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--only", choices=["all", "prefill", "decode", "headline"], default="all")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="first run one plain 1 GiB device-to-device copy: the known-size kernel "
+                         "that scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings to bytes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -189,6 +192,14 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     ak.load_extension()
     torch.manual_seed(0)
+    if args.calib_copy:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        torch.cuda.empty_cache()
     K, W = args.steps, args.warmup
     headline = prefill_case(2, 32, 8192, 128, True, K, W)
     log(json.dumps(headline))

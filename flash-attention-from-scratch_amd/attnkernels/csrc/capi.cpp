@@ -51,7 +51,9 @@ int prefill(const char* who, const void* q, const void* k, const void* v, void* 
     a.n = seq_len;
     a.d = (int)head_dim;
     a.causal = causal != 0;
-    a.sl2 = (float)(std::fabs(scale) * kLog2e);
+    // |scale| * log2(e), kept >= 1e-30 so that masked scores (-inf) still map to
+    // 2^-inf = 0; below that every score rounds to the same weight anyway.
+    a.sl2 = (float)std::fmax(std::fabs(scale) * kLog2e, 1e-30);
     a.qflip = std::signbit(scale) && scale != 0.0 ? 0x80008000u : 0u;
     a.stream = stream;
     return hip_status(ak::prefill_launch(a), who);

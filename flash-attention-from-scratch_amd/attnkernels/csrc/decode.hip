@@ -187,36 +187,64 @@ paged_decode_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const
     }
 }
 
-// One wave per (sequence, query head).  ns = ceil(ctx/P) partials are merged
-// (paged_decode.cu:204-215); ns is clamped to the number of launched splits.
+// LSE merge of the split partials (paged_decode.cu:204-215): one 256-thread
+// workgroup per (sequence, query head) row; ns = ceil(ctx/P) partials are
+// merged, clamped to the number of launched splits.  Every partial is read by
+// an independent load (no serial chain over splits): pass 1 takes the block
+// max of m; pass 2 has D/4 threads per partial row, each with a float4 of o,
+// and 256/(D/4) partial rows in flight per step; the groups are summed in LDS.
 template <int D>
-__global__ void __launch_bounds__(64)
+__global__ void __launch_bounds__(256)
 paged_reduce_kernel(const float* __restrict__ o_part, const float* __restrict__ m_part,
                     const float* __restrict__ l_part, const int* __restrict__ ctx_lens,
                     f16* __restrict__ out, int hq, int partition, int num_splits) {
-    constexpr int PER = D / kWave;
+    constexpr int THREADS = 256, TPR = D / 4, GROUPS = THREADS / TPR;
+    __shared__ float red_max[THREADS / kWave];
+    __shared__ f32x4 red_acc[GROUPS][TPR];
+    __shared__ float red_den[GROUPS];
     const size_t row = blockIdx.x;
     const int b = (int)(row / hq);
     const int ctx = ctx_lens[b];
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     int ns = ctx > 0 ? (int)(((long long)ctx + partition - 1) / partition) : 0;
     ns = min(ns, num_splits);
     const float* mp = m_part + row * num_splits;
     const float* lp = l_part + row * num_splits;
-    const float* op = o_part + row * num_splits * D;
+    const f32x4* op = reinterpret_cast<const f32x4*>(o_part + row * num_splits * D);
+
     float M = -INFINITY;
-    for (int s = 0; s < ns; ++s) M = fmaxf(M, mp[s]);
-    float num[PER], den = 0.f;
+    for (int s = tid; s < ns; s += THREADS) M = fmaxf(M, mp[s]);
 #pragma unroll
-    for (int j = 0; j < PER; ++j) num[j] = 0.f;
-    for (int s = 0; s < ns; ++s) {
+    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, kWave));
+    if (lane == 0) red_max[w] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(red_max[0], red_max[1]), fmaxf(red_max[2], red_max[3]));
+
+    const int g = tid / TPR, j = tid % TPR;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    float den = 0.f;
+#pragma unroll 4
+    for (int s = g; s < ns; s += GROUPS) {
         const float wgt = lp[s] * exp2_fast(mp[s] - M);
-#pragma unroll
-        for (int j = 0; j < PER; ++j) num[j] = fmaf(wgt, op[(size_t)s * D + lane + j * kWave], num[j]);
+        acc += wgt * op[(size_t)s * TPR + j];
         den += wgt;
     }
+    red_acc[g][j] = acc;
+    if (j == 0) red_den[g] = den;
+    __syncthreads();
+    if (tid < TPR) {
+        f32x4 sum = red_acc[0][tid];
+        float dsum = red_den[0];
 #pragma unroll
-    for (int j = 0; j < PER; ++j) out[row * D + lane + j * kWave] = (f16)(ns > 0 ? num[j] / den : 0.f);
+        for (int k = 1; k < GROUPS; ++k) {
+            sum += red_acc[k][tid];
+            dsum += red_den[k];
+        }
+        const float inv = ns > 0 ? 1.f / dsum : 0.f;
+        f16* dst = out + row * D + tid * 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[i] = (f16)(sum[i] * inv);
+    }
 }
 
 template <int D, int G>
@@ -233,7 +261,7 @@ static hipError_t launch_decode(const DecodeArgs& a) {
                        (int)a.max_blocks, (int)a.num_blocks, (int)a.partition, (int)a.num_splits, a.sl2);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.num_splits == 1) return e;
-    hipLaunchKernelGGL((paged_reduce_kernel<D>), dim3((unsigned)(a.batch * a.hq)), dim3(kWave), 0, stream,
+    hipLaunchKernelGGL((paged_reduce_kernel<D>), dim3((unsigned)(a.batch * a.hq)), dim3(256), 0, stream,
                        a.o_part, a.m_part, a.l_part, a.context_lens, (f16*)a.out, (int)a.hq,
                        (int)a.partition, (int)a.num_splits);
     return hipGetLastError();

@@ -62,7 +62,9 @@ struct Staged {
     f16x8 v[4];
 };
 
-// Global -> registers for key tile [k0, k0 + BN).  Rows past n read as zero.
+// Global -> registers for key tile [k0, k0 + BN).  Rows past n are clamped to
+// row n-1 instead of predicated: the loads stay branch-free and in bounds, and
+// the scores of those keys are masked to -inf, so their P is exactly 0.
 template <int D>
 __device__ __forceinline__ void stage_load(Staged<D>& st, const f16* __restrict__ kb,
                                            const f16* __restrict__ vb, int k0, int n, int tid) {
@@ -71,14 +73,14 @@ __device__ __forceinline__ void stage_load(Staged<D>& st, const f16* __restrict_
     for (int j = 0; j < T::KLOADS; ++j) {
         const int c = tid + j * T::THREADS;
         const int row = c / T::CH, ch = c % T::CH;
-        const int key = k0 + row;
-        st.k[j] = key < n ? *reinterpret_cast<const f16x8*>(kb + (size_t)key * D + ch * 8) : f16x8{};
+        const int key = min(k0 + row, n - 1);
+        st.k[j] = *reinterpret_cast<const f16x8*>(kb + (size_t)key * D + ch * 8);
     }
     const int dc = tid % T::CH, kg = tid / T::CH;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int key = k0 + kg * 4 + j;
-        st.v[j] = key < n ? *reinterpret_cast<const f16x8*>(vb + (size_t)key * D + dc * 8) : f16x8{};
+        const int key = min(k0 + kg * 4 + j, n - 1);
+        st.v[j] = *reinterpret_cast<const f16x8*>(vb + (size_t)key * D + dc * 8);
     }
 }
 
@@ -105,9 +107,96 @@ __device__ __forceinline__ void stage_store(const Staged<D>& st, f16* __restrict
     }
 }
 
-// Value of lane l^32 combined with this lane's by max / sum.
-__device__ __forceinline__ float pair_max(float x) { return fmaxf(x, shfl_xor<32>(x)); }
-__device__ __forceinline__ float pair_sum(float x) { return x + shfl_xor<32>(x); }
+// {own value, value of lane l^32} in some order, by v_permlane32_swap on two
+// copies of x (no LDS traffic).  Issued as inline asm: with the builtin and
+// identical inputs the compiler kept only one of the two swapped registers.
+// The s_nop covers the VALU-write -> permlane-read hazard.
+__device__ __forceinline__ f32x2 pair_values(float x) {
+    float a = x, b = x;
+    asm volatile("s_nop 2\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return f32x2{a, b};
+}
+__device__ __forceinline__ float pair_max(float x) {
+    const f32x2 v = pair_values(x);
+    return fmaxf(v[0], v[1]);
+}
+__device__ __forceinline__ float pair_sum(float x) {
+    const f32x2 v = pair_values(x);
+    return v[0] + v[1];
+}
+
+// The subtracted row maximum only moves when the tile's maximum exceeds it by
+// more than this many powers of two, so O is rescaled rarely.  Softmax is
+// invariant to the value subtracted; P stays <= 2^8, exact enough in fp16.
+constexpr float kRescaleSlack = 8.f;
+
+// One key tile for one wave: S^T = K Q^T, online softmax, O^T += V^T P^T.
+template <int D, bool CAUSAL, bool MASK>
+__device__ __forceinline__ void tile_step(const f16* __restrict__ ks, const f16* __restrict__ vs,
+                                          const f16x8 (&qf)[PrefillTile<D>::DC], f32x16 (&o)[PrefillTile<D>::DT],
+                                          float& ms_run, float& l_run, int k0, int n, int qrow, int col,
+                                          int half, float sl2) {
+    using T = PrefillTile<D>;
+    // S^T: KB blocks of 32 keys x 32 queries.
+    f32x16 s[T::KB];
+#pragma unroll
+    for (int b = 0; b < T::KB; ++b) {
+        s[b] = f32x16{};
+        const f16* krow = ks + (b * 32 + col) * T::LDK + half * 8;
+#pragma unroll
+        for (int dc = 0; dc < T::DC; ++dc)
+            s[b] = mfma32x32x16(*reinterpret_cast<const f16x8*>(krow + dc * 16), qf[dc], s[b]);
+    }
+    if constexpr (MASK) {  // keys past n and, if causal, keys after the query
+#pragma unroll
+        for (int b = 0; b < T::KB; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = k0 + b * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+                if (key >= n || (CAUSAL && key > qrow)) s[b][r] = -INFINITY;
+            }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < T::KB; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
+    const float mxs = pair_max(mx) * sl2;  // this tile's scaled row max (-inf if all masked)
+    const bool grow = mxs > ms_run + kRescaleSlack;  // always true on the first tile
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+        const float ms_new = grow ? mxs : ms_run;
+        const float alpha = exp2_fast(ms_run - ms_new);  // 0 on the first tile, 1 if unchanged
+        ms_run = ms_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int t = 0; t < T::DT; ++t) o[t] *= alpha;
+    }
+    float psum = 0.f;
+#pragma unroll
+    for (int b = 0; b < T::KB; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float p = exp2_fast(fmaf(s[b][r], sl2, -ms_run));  // masked: 2^-inf = 0
+            s[b][r] = p;
+            psum += p;
+        }
+    l_run += psum;
+
+    // P^T as the B operand: k-step c = accumulator regs 8*(c%2).. of block c/2.
+    f16x8 pf[T::PC];
+#pragma unroll
+    for (int c = 0; c < T::PC; ++c)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pf[c][i] = (f16)s[c >> 1][(c & 1) * 8 + i];
+    // O^T += V^T P^T.
+#pragma unroll
+    for (int t = 0; t < T::DT; ++t) {
+        const f16* vrow = vs + (t * 32 + col) * T::LDV + half * 8;
+#pragma unroll
+        for (int c = 0; c < T::PC; ++c)
+            o[t] = mfma32x32x16(*reinterpret_cast<const f16x8*>(vrow + c * 16), pf[c], o[t]);
+    }
+}
 
 template <int D, bool CAUSAL>
 __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const f16* __restrict__ kb,
@@ -125,7 +214,8 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
     f16x8 qf[T::DC];
 #pragma unroll
     for (int dc = 0; dc < T::DC; ++dc) {
-        f16x8 x = qrow < n ? *reinterpret_cast<const f16x8*>(qb + (size_t)qrow * D + dc * 16 + half * 8) : f16x8{};
+        // Rows past n are clamped to n-1: computed, never stored.
+        f16x8 x = *reinterpret_cast<const f16x8*>(qb + (size_t)min(qrow, n - 1) * D + dc * 16 + half * 8);
         if (qflip) {  // negative scale: fold the sign into Q exactly
             typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
             x = __builtin_bit_cast(f16x8, __builtin_bit_cast(u32x4, x) ^ qflip);
@@ -136,8 +226,7 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
     f32x16 o[T::DT];
 #pragma unroll
     for (int t = 0; t < T::DT; ++t) o[t] = f32x16{};
-    float m_run = -INFINITY;  // running max of raw scores
-    float ms_run = -INFINITY; // the scaled max actually subtracted so far
+    float ms_run = -INFINITY; // the scaled row maximum subtracted so far
     float l_run = 0.f;        // this lane's share of the row sum
 
     const int kend = CAUSAL ? min(n, q0 + T::BM) : n;
@@ -157,66 +246,11 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
 
         const bool active = !CAUSAL || k0 <= qw0 + T::QW - 1;
         if (active) {
-            // S^T = K Q^T: KB blocks of 32 keys x 32 queries.
-            f32x16 s[T::KB];
-#pragma unroll
-            for (int b = 0; b < T::KB; ++b) {
-                s[b] = f32x16{};
-                const f16* krow = ks + (b * 32 + col) * T::LDK + half * 8;
-#pragma unroll
-                for (int dc = 0; dc < T::DC; ++dc)
-                    s[b] = mfma32x32x16(*reinterpret_cast<const f16x8*>(krow + dc * 16), qf[dc], s[b]);
-            }
-            // Mask keys past n and, if causal, keys after the query.
             const bool need_mask = (k0 + T::BN > n) || (CAUSAL && k0 + T::BN - 1 > qw0);
-            if (need_mask) {
-#pragma unroll
-                for (int b = 0; b < T::KB; ++b)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int key = k0 + b * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-                        if (key >= n || (CAUSAL && key > qrow)) s[b][r] = -INFINITY;
-                    }
-            }
-            float mx = -INFINITY;
-#pragma unroll
-            for (int b = 0; b < T::KB; ++b)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
-            mx = pair_max(mx);
-            const float m_new = fmaxf(m_run, mx);
-            const float ms_new = (m_new == -INFINITY) ? 0.f : m_new * sl2;
-            const float alpha = exp2_fast(ms_run - ms_new);
-            m_run = m_new;
-            ms_run = ms_new;
-            float psum = 0.f;
-#pragma unroll
-            for (int b = 0; b < T::KB; ++b)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    float p = exp2_fast(fmaf(s[b][r], sl2, -ms_new));
-                    if (need_mask) p = (s[b][r] == -INFINITY) ? 0.f : p;
-                    s[b][r] = p;
-                    psum += p;
-                }
-            l_run = l_run * alpha + psum;
-#pragma unroll
-            for (int t = 0; t < T::DT; ++t) o[t] *= alpha;
-
-            // P^T as the B operand: k-step c = accumulator regs 8*(c%2).. of block c/2.
-            f16x8 pf[T::PC];
-#pragma unroll
-            for (int c = 0; c < T::PC; ++c)
-#pragma unroll
-                for (int i = 0; i < 8; ++i) pf[c][i] = (f16)s[c >> 1][(c & 1) * 8 + i];
-            // O^T += V^T P^T.
-#pragma unroll
-            for (int t = 0; t < T::DT; ++t) {
-                const f16* vrow = vs + (t * 32 + col) * T::LDV + half * 8;
-#pragma unroll
-                for (int c = 0; c < T::PC; ++c)
-                    o[t] = mfma32x32x16(*reinterpret_cast<const f16x8*>(vrow + c * 16), pf[c], o[t]);
-            }
+            if (need_mask)
+                tile_step<D, CAUSAL, true>(ks, vs, qf, o, ms_run, l_run, k0, n, qrow, col, half, sl2);
+            else
+                tile_step<D, CAUSAL, false>(ks, vs, qf, o, ms_run, l_run, k0, n, qrow, col, half, sl2);
         }
         if (more) {
             f16* nks = lds + ((kt + 1) & 1) * T::STAGE;
