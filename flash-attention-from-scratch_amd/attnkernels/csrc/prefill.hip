@@ -52,6 +52,7 @@ struct PrefillTile {
     static constexpr int DT = D / 32;            // 32-row tiles of O^T
     static constexpr int PC = BN / 16;           // k-steps of V^T P^T
     static constexpr int KLOADS = BN * CH / THREADS;  // 16-byte K loads per thread (4)
+    static constexpr int KG = BN / 4;            // groups of 4 keys in a tile (V staging)
     static_assert(KLOADS == 4, "each thread stages 4 K chunks and 4 V rows per tile");
     static_assert(D % 32 == 0 && BN % 32 == 0, "tile shapes");
 };
@@ -76,7 +77,7 @@ __device__ __forceinline__ void stage_load(Staged<D>& st, const f16* __restrict_
         const int key = min(k0 + row, n - 1);
         st.k[j] = *reinterpret_cast<const f16x8*>(kb + (size_t)key * D + ch * 8);
     }
-    const int dc = tid % T::CH, kg = tid / T::CH;
+    const int kg = tid % T::KG, dc = tid / T::KG;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int key = min(k0 + kg * 4 + j, n - 1);
@@ -95,7 +96,9 @@ __device__ __forceinline__ void stage_store(const Staged<D>& st, f16* __restrict
         const int row = c / T::CH, ch = c % T::CH;
         *reinterpret_cast<f16x8*>(ks + row * T::LDK + ch * 8) = st.k[j];
     }
-    const int dc = tid % T::CH, kg = tid / T::CH;
+    // Lanes t..t+15 hold consecutive key groups of the same 8 head dims, so each
+    // 8-byte store instruction fills one whole V^T row: no bank conflicts.
+    const int kg = tid % T::KG, dc = tid / T::KG;
     const int kl = kg * 4;                                  // first of 4 keys, multiple of 4
     const int pos = (kl & ~15) | swap23(kl & 15);           // its slot in the V^T row
 #pragma unroll
@@ -123,6 +126,17 @@ __device__ __forceinline__ float pair_max(float x) {
 __device__ __forceinline__ float pair_sum(float x) {
     const f32x2 v = pair_values(x);
     return v[0] + v[1];
+}
+
+// v *= a without moving v to new registers: as plain C++ the conditional
+// rescale below made the compiler copy all O accumulators on every tile.
+__device__ __forceinline__ void scale_in_place(f32x16& v, float a) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        float x = v[i];
+        asm volatile("v_mul_f32 %0, %0, %1" : "+v"(x) : "v"(a));
+        v[i] = x;
+    }
 }
 
 // The subtracted row maximum only moves when the tile's maximum exceeds it by
@@ -163,24 +177,22 @@ __device__ __forceinline__ void tile_step(const f16* __restrict__ ks, const f16*
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
     const float mxs = pair_max(mx) * sl2;  // this tile's scaled row max (-inf if all masked)
     const bool grow = mxs > ms_run + kRescaleSlack;  // always true on the first tile
-    if (__builtin_amdgcn_ballot_w64(grow)) {
-        const float ms_new = grow ? mxs : ms_run;
-        const float alpha = exp2_fast(ms_run - ms_new);  // 0 on the first tile, 1 if unchanged
-        ms_run = ms_new;
-        l_run *= alpha;
+    const float ms_new = grow ? mxs : ms_run;
+    const float alpha = exp2_fast(ms_run - ms_new);  // 0 on the first tile, 1 if unchanged
+    ms_run = ms_new;
+    l_run *= alpha;
 #pragma unroll
-        for (int t = 0; t < T::DT; ++t) o[t] *= alpha;
-    }
-    float psum = 0.f;
+    for (int t = 0; t < T::DT; ++t) o[t] *= alpha;
+    float ps[4] = {0.f, 0.f, 0.f, 0.f};  // 4 independent chains instead of one serial sum
 #pragma unroll
     for (int b = 0; b < T::KB; ++b)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const float p = exp2_fast(fmaf(s[b][r], sl2, -ms_run));  // masked: 2^-inf = 0
             s[b][r] = p;
-            psum += p;
+            ps[r & 3] += p;
         }
-    l_run += psum;
+    l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
 
     // P^T as the B operand: k-step c = accumulator regs 8*(c%2).. of block c/2.
     f16x8 pf[T::PC];
@@ -231,27 +243,36 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
 
     const int kend = CAUSAL ? min(n, q0 + T::BM) : n;
     const int nkt = (kend + T::BN - 1) / T::BN;
+    // Tiles before kt_mask need no masking for any wave of the workgroup: all
+    // their keys are < n and (causal) <= the workgroup's first query row.
+    const int kt_mask = min(nkt, CAUSAL ? q0 / T::BN : n / T::BN);
 
     Staged<D> st;
     stage_load<D>(st, kb, vb, 0, n, tid);
     stage_store<D>(st, lds, lds + T::K_ELEMS, tid);
     __syncthreads();
 
-    for (int kt = 0; kt < nkt; ++kt) {
+    // Two loops with one tile body each (unmasked, then the diagonal/tail tiles
+    // with masking), so that O stays in the same registers across iterations.
+    for (int kt = 0; kt < kt_mask; ++kt) {
+        f16* ks = lds + (kt & 1) * T::STAGE;
+        const bool more = kt + 1 < nkt;
+        if (more) stage_load<D>(st, kb, vb, (kt + 1) * T::BN, n, tid);
+        tile_step<D, CAUSAL, false>(ks, ks + T::K_ELEMS, qf, o, ms_run, l_run, kt * T::BN, n, qrow, col, half,
+                                    sl2);
+        if (more) {
+            f16* nks = lds + ((kt + 1) & 1) * T::STAGE;
+            stage_store<D>(st, nks, nks + T::K_ELEMS, tid);
+        }
+        __syncthreads();
+    }
+    for (int kt = kt_mask; kt < nkt; ++kt) {
         const int k0 = kt * T::BN;
         f16* ks = lds + (kt & 1) * T::STAGE;
-        f16* vs = ks + T::K_ELEMS;
         const bool more = kt + 1 < nkt;
         if (more) stage_load<D>(st, kb, vb, k0 + T::BN, n, tid);
-
-        const bool active = !CAUSAL || k0 <= qw0 + T::QW - 1;
-        if (active) {
-            const bool need_mask = (k0 + T::BN > n) || (CAUSAL && k0 + T::BN - 1 > qw0);
-            if (need_mask)
-                tile_step<D, CAUSAL, true>(ks, vs, qf, o, ms_run, l_run, k0, n, qrow, col, half, sl2);
-            else
-                tile_step<D, CAUSAL, false>(ks, vs, qf, o, ms_run, l_run, k0, n, qrow, col, half, sl2);
-        }
+        if (!CAUSAL || k0 <= qw0 + T::QW - 1)  // else every key of the tile is after this wave's rows
+            tile_step<D, CAUSAL, true>(ks, ks + T::K_ELEMS, qf, o, ms_run, l_run, k0, n, qrow, col, half, sl2);
         if (more) {
             f16* nks = lds + ((kt + 1) & 1) * T::STAGE;
             stage_store<D>(st, nks, nks + T::K_ELEMS, tid);
