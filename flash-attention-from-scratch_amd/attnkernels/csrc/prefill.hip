@@ -177,29 +177,34 @@ __device__ __forceinline__ void tile_step(const f16* __restrict__ ks, const f16*
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
     const float mxs = pair_max(mx) * sl2;  // this tile's scaled row max (-inf if all masked)
     const bool grow = mxs > ms_run + kRescaleSlack;  // always true on the first tile
-    const float ms_new = grow ? mxs : ms_run;
-    const float alpha = exp2_fast(ms_run - ms_new);  // 0 on the first tile, 1 if unchanged
-    ms_run = ms_new;
-    l_run *= alpha;
+    if (__builtin_amdgcn_ballot_w64(grow)) {          // rare after the first tile
+        const float ms_new = grow ? mxs : ms_run;
+        const float alpha = exp2_fast(ms_run - ms_new);  // 0 on the first tile, 1 if unchanged
+        ms_run = ms_new;
+        l_run *= alpha;
 #pragma unroll
-    for (int t = 0; t < T::DT; ++t) o[t] *= alpha;
-    float ps[4] = {0.f, 0.f, 0.f, 0.f};  // 4 independent chains instead of one serial sum
+        for (int t = 0; t < T::DT; ++t) o[t] *= alpha;
+    }
 #pragma unroll
     for (int b = 0; b < T::KB; ++b)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float p = exp2_fast(fmaf(s[b][r], sl2, -ms_run));  // masked: 2^-inf = 0
-            s[b][r] = p;
-            ps[r & 3] += p;
-        }
-    l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+        for (int r = 0; r < 16; ++r) s[b][r] = exp2_fast(fmaf(s[b][r], sl2, -ms_run));  // masked: 2^-inf = 0
 
     // P^T as the B operand: k-step c = accumulator regs 8*(c%2).. of block c/2.
+    // The row sum is taken over the same fp16 values the MFMA consumes, two at
+    // a time by v_dot2_f32_f16 against (1, 1), in 4 independent chains.
     f16x8 pf[T::PC];
+    float ps[4] = {0.f, 0.f, 0.f, 0.f};
+    const f16x2 ones = {(f16)1.f, (f16)1.f};
 #pragma unroll
-    for (int c = 0; c < T::PC; ++c)
+    for (int c = 0; c < T::PC; ++c) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) pf[c][i] = (f16)s[c >> 1][(c & 1) * 8 + i];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            ps[i] = __builtin_amdgcn_fdot2(f16x2{pf[c][2 * i], pf[c][2 * i + 1]}, ones, ps[i], false);
+    }
+    l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
     // O^T += V^T P^T.
 #pragma unroll
     for (int t = 0; t < T::DT; ++t) {
