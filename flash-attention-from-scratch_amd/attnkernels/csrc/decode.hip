@@ -83,25 +83,36 @@ paged_decode_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const
     const size_t page_stride = (size_t)hkv * bs * D;
     const size_t head_off = (size_t)kvh * bs * D + li * 8;
 
-    for (int t0 = start + w * T::TOK; t0 < end; t0 += T::NW * T::TOK) {
+    // Page ids of this lane's tokens in the chunk starting at t0 (-1 past the
+    // split).  They are loaded one chunk ahead, behind the current chunk's K/V
+    // loads, so a chunk costs one memory round trip instead of two.
+    auto load_pages = [&](int t0, int (&pg)[T::U]) {
+#pragma unroll
+        for (int u = 0; u < T::U; ++u) {
+            const int t = t0 + u * T::TPL + gi;
+            const int pi = bs_shift >= 0 ? (t >> bs_shift) : (t / bs);
+            pg[u] = t < end ? bt[pi] : -1;
+        }
+    };
+    const int stride = T::NW * T::TOK;
+    int pg[T::U];
+    load_pages(start + w * T::TOK, pg);
+
+    for (int t0 = start + w * T::TOK; t0 < end; t0 += stride) {
         f16x8 kr[T::U], vr[T::U];
         bool valid[T::U];
 #pragma unroll
         for (int u = 0; u < T::U; ++u) {
             const int t = t0 + u * T::TPL + gi;
-            bool ok = t < end;
-            size_t off = 0;
-            if (ok) {
-                const int pi = bs_shift >= 0 ? (t >> bs_shift) : (t / bs);
-                const int po = t - pi * bs;
-                const int page = bt[pi];
-                ok = (unsigned)page < (unsigned)num_blocks;  // a bad page id is never read
-                off = (size_t)page * page_stride + head_off + (size_t)po * D;
-            }
+            const int po = bs_shift >= 0 ? (t & (bs - 1)) : (t % bs);
+            const bool ok = t < end && (unsigned)pg[u] < (unsigned)num_blocks;  // bad page ids are never read
+            const size_t off = (size_t)(ok ? pg[u] : 0) * page_stride + head_off + (size_t)po * D;
             valid[u] = ok;
-            kr[u] = ok ? *reinterpret_cast<const f16x8*>(kc + off) : f16x8{};
-            vr[u] = ok ? *reinterpret_cast<const f16x8*>(vc + off) : f16x8{};
+            // K/V are streamed once: non-temporal loads keep them out of the caches' way.
+            kr[u] = ok ? __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(kc + off)) : f16x8{};
+            vr[u] = ok ? __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(vc + off)) : f16x8{};
         }
+        load_pages(t0 + stride, pg);
 #pragma unroll
         for (int h = 0; h < G; ++h) {
             float s[T::U];
