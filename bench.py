@@ -175,7 +175,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--only", choices=["all", "prefill", "decode", "headline"], default="all")
+    ap.add_argument("--only", default="all",
+                    help="all | headline | prefill | decode | comma list of workload names")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first run one plain 1 GiB device-to-device copy: the known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings to bytes")
@@ -201,19 +202,31 @@ def main():
         del src, dst
         torch.cuda.empty_cache()
     K, W = args.steps, args.warmup
-    headline = prefill_case(2, 32, 8192, 128, True, K, W)
-    log(json.dumps(headline))
-    workloads = []
-    if args.only in ("all", "prefill"):
-        for cfg in [(4, 16, 2048, 64, False), (2, 32, 8191, 128, True)]:
-            workloads.append(prefill_case(*cfg, K, W))
-            log(json.dumps(workloads[-1]))
-    if args.only in ("all", "decode"):
-        lens4 = torch.randint(1, 4097, (64,), generator=torch.Generator().manual_seed(4)).tolist()
-        for lens, d, part in [(lens4, 128, 512), ([32768] * 8, 128, 256), ([32768] * 8, 64, 256)]:
-            workloads.append(decode_case(lens, 32, d, 16, part, K, W))
-            log(json.dumps(workloads[-1]))
+    lens4 = torch.randint(1, 4097, (64,), generator=torch.Generator().manual_seed(4)).tolist()
+    cases = {  # BASELINE.json configs[1..4]
+        "prefill_d128_n8192_causal": lambda: prefill_case(2, 32, 8192, 128, True, K, W),
+        "prefill_d64_n2048": lambda: prefill_case(4, 16, 2048, 64, False, K, W),
+        "prefill_d128_n8191_causal": lambda: prefill_case(2, 32, 8191, 128, True, K, W),
+        "decode_ragged64_d128": lambda: decode_case(lens4, 32, 128, 16, 512, K, W),
+        "decode_long8_d128": lambda: decode_case([32768] * 8, 32, 128, 16, 256, K, W),
+        "decode_long8_d64": lambda: decode_case([32768] * 8, 32, 64, 16, 256, K, W),
+    }
+    groups = {"all": list(cases), "headline": ["prefill_d128_n8192_causal"],
+              "prefill": [c for c in cases if c.startswith("prefill")],
+              "decode": ["prefill_d128_n8192_causal"] + [c for c in cases if c.startswith("decode")]}
+    selected = groups.get(args.only, [c for c in args.only.split(",") if c in cases])
+    if not selected:
+        raise SystemExit(f"--only: choose from {sorted(groups)} or a comma list of {sorted(cases)}")
+    results = {}
+    for name in selected:
+        results[name] = cases[name]()
+        log(json.dumps(results[name]))
+    headline = results.get("prefill_d128_n8192_causal")
+    workloads = [dict(name=k, **v) for k, v in results.items() if k != "prefill_d128_n8192_causal"]
     cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
+    if headline is None:  # a profiling run of other workloads: report them only
+        print(json.dumps({"workloads": workloads, "cpu_baseline": cpu}), flush=True)
+        return
     ach = headline["kernel_tflops"]
     line = {
         "metric": "prefill TFLOP/s (% MFMA peak); paged decode KV GB/s (% HBM peak)",

@@ -129,6 +129,7 @@ int ak_paged_decode(const void* q, const void* k_cache, const void* v_cache, con
         max_blocks_per_seq * block_size > INT_MAX || batch > 65535 || num_kv_heads > 65535)
         return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: size out of range");
     const int64_t splits = (max_context_len + partition - 1) / partition;
+    if (splits > 65535) return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: more than 65535 splits");
     ak::DecodeArgs a{};
     if (splits > 1) {
         const size_t need = ak_paged_decode_workspace_size(batch, num_heads, head_dim, max_context_len, partition);

@@ -56,20 +56,42 @@ paged_decode_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const
     __shared__ float red_acc[T::NW][G][D];
     __shared__ float red_m[T::NW][G], red_l[T::NW][G];
 
-    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    // kv head fastest: neighbouring workgroups read neighbouring 4 KB head
+    // blocks of the same pages.
+    const int kvh = blockIdx.x, split = blockIdx.y, b = blockIdx.z;
     const int hq = hkv * G;
-    const int ctx = min(ctx_lens[b], max_blocks * bs);  // never index past the table row
     const int start = split * partition;
-    if (start >= ctx) return;  // whole workgroup: this split is past the context
-    const int end = min(ctx, start + partition);
     const int tid = threadIdx.x, lane = tid & 63, w = uniform(tid >> 6);
     const int gi = lane / T::LPT, li = lane % T::LPT;
+    const int* bt = block_tables + (size_t)b * max_blocks;
+    const int max_tok = max_blocks * bs;  // never index past the table row
 
-    // q for the G heads of this kv head, raw fp16 (scaled after the dot product).
-    f16x8 qv[G];
+    // Page ids of this lane's tokens in the chunk starting at t0, for tokens
+    // below lim (-1 elsewhere).  They are loaded one chunk ahead, behind the
+    // current chunk's K/V loads, so a chunk costs one memory round trip.
+    auto load_pages = [&](int t0, int lim, int (&pg)[T::U]) {
+#pragma unroll
+        for (int u = 0; u < T::U; ++u) {
+            const int t = t0 + u * T::TPL + gi;
+            const int pi = bs_shift >= 0 ? (t >> bs_shift) : (t / bs);
+            pg[u] = t < lim ? bt[pi] : -1;
+        }
+    };
+    // The context length, q and the first chunk's page ids are loaded together:
+    // the page loads are bounded by the table row, not by the (not yet known)
+    // context length, which only masks them afterwards.
+    const int ctx_raw = ctx_lens[b];
+    f16x8 qv[G];  // q of the G heads of this kv head, raw fp16 (scaled after the dot product)
 #pragma unroll
     for (int h = 0; h < G; ++h)
         qv[h] = *reinterpret_cast<const f16x8*>(q + ((size_t)b * hq + kvh * G + h) * D + li * 8);
+    const int stride = T::NW * T::TOK;
+    int pg[T::U];
+    load_pages(start + w * T::TOK, min(start + partition, max_tok), pg);
+
+    const int ctx = min(ctx_raw, max_tok);
+    if (start >= ctx) return;  // whole workgroup: this split is past the context
+    const int end = min(ctx, start + partition);
 
     float m[G], l[G], acc[G][8];
 #pragma unroll
@@ -79,24 +101,8 @@ paged_decode_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[h][i] = 0.f;
     }
-    const int* bt = block_tables + (size_t)b * max_blocks;
     const size_t page_stride = (size_t)hkv * bs * D;
     const size_t head_off = (size_t)kvh * bs * D + li * 8;
-
-    // Page ids of this lane's tokens in the chunk starting at t0 (-1 past the
-    // split).  They are loaded one chunk ahead, behind the current chunk's K/V
-    // loads, so a chunk costs one memory round trip instead of two.
-    auto load_pages = [&](int t0, int (&pg)[T::U]) {
-#pragma unroll
-        for (int u = 0; u < T::U; ++u) {
-            const int t = t0 + u * T::TPL + gi;
-            const int pi = bs_shift >= 0 ? (t >> bs_shift) : (t / bs);
-            pg[u] = t < end ? bt[pi] : -1;
-        }
-    };
-    const int stride = T::NW * T::TOK;
-    int pg[T::U];
-    load_pages(start + w * T::TOK, pg);
 
     for (int t0 = start + w * T::TOK; t0 < end; t0 += stride) {
         f16x8 kr[T::U], vr[T::U];
@@ -112,7 +118,7 @@ paged_decode_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const
             kr[u] = ok ? __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(kc + off)) : f16x8{};
             vr[u] = ok ? __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(vc + off)) : f16x8{};
         }
-        load_pages(t0 + stride, pg);
+        load_pages(t0 + stride, end, pg);
 #pragma unroll
         for (int h = 0; h < G; ++h) {
             float s[T::U];
@@ -265,7 +271,7 @@ static hipError_t launch_decode(const DecodeArgs& a) {
     for (int s = 0; s < 31; ++s)
         if ((int64_t(1) << s) == a.bs) bs_shift = s;
     const hipStream_t stream = (hipStream_t)a.stream;
-    dim3 grid((unsigned)a.num_splits, (unsigned)a.hkv, (unsigned)a.batch);
+    dim3 grid((unsigned)a.hkv, (unsigned)a.num_splits, (unsigned)a.batch);
     hipLaunchKernelGGL((paged_decode_kernel<D, G>), grid, dim3(T::THREADS), 0, stream, (const f16*)a.q,
                        (const f16*)a.k_cache, (const f16*)a.v_cache, a.block_tables, a.context_lens,
                        (f16*)a.out, a.o_part, a.m_part, a.l_part, (int)a.hkv, (int)a.bs, bs_shift,
