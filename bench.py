@@ -35,6 +35,16 @@ for _p in (str(ROOT), str(ROOT / "flash-attention-from-scratch_amd")):
 
 PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+# HBM bytes per launch of each workload's dominant kernel, from the committed
+# rocprofv3 FETCH_SIZE/WRITE_SIZE passes (scaled by a 1 GiB copy; see profiles/).
+TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
+
+
+def measured_traffic(name):
+    try:
+        return json.loads(TRAFFIC_FILE.read_text()).get(name)
+    except (OSError, ValueError):
+        return None
 
 
 def log(msg):
@@ -222,7 +232,17 @@ def main():
         results[name] = cases[name]()
         log(json.dumps(results[name]))
     headline = results.get("prefill_d128_n8192_causal")
-    workloads = [dict(name=k, **v) for k, v in results.items() if k != "prefill_d128_n8192_causal"]
+    workloads = []
+    for k, v in results.items():
+        if k == "prefill_d128_n8192_causal":
+            continue
+        t = measured_traffic(k)
+        hbm = v["unit"] == "GB/s"
+        ach = v["kernel_gbs"] if hbm else v["kernel_tflops"]
+        peak = PEAK_HBM_GBS if hbm else PEAK_FP16_TFLOPS
+        workloads.append(dict(name=k, **v, roofline={
+            "bound": "hbm" if hbm else "mfma", "achieved": ach, "peak": peak, "unit": v["unit"],
+            "frac": round(ach / peak, 4), "traffic": t["traffic_bytes"] if t else None}))
     cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
     if headline is None:  # a profiling run of other workloads: report them only
         print(json.dumps({"workloads": workloads, "cpu_baseline": cpu}), flush=True)
@@ -237,7 +257,9 @@ def main():
                    "seq_len": 8192, "heads": 32, "head_dim": 128, "causal": True, "parallelism": "none"},
         "max_abs_err": headline["max_abs_err"],
         "roofline": {"bound": "mfma", "achieved": ach, "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(ach / PEAK_FP16_TFLOPS, 4), "traffic": None,
+                     "frac": round(ach / PEAK_FP16_TFLOPS, 4),
+                     "traffic": (measured_traffic("prefill_d128_n8192_causal") or {}).get("traffic_bytes"),
+                     "traffic_source": "profiles/traffic.json (rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-scaled)",
                      "kernel": "flash_prefill_kernel<128,true>",
                      "kernel_ms_mean": headline["kernel_ms_mean"]},
         "cpu_baseline": cpu,
