@@ -9,21 +9,24 @@
 //   * A workgroup is 4 waves and owns BM = 128 query rows of one (batch, head);
 //     each wave owns 32 of them, so no softmax row is shared between waves.
 //   * Scores are computed transposed, S^T = K Q^T, with K as the MFMA A operand
-//     (straight 16-byte LDS reads of K rows) and Q as the B operand (kept in
-//     VGPRs for the whole kernel).  In the accumulator a lane then holds one
-//     query column and 16 keys per 32x32 block, so the row max / sum are
-//     in-lane plus one exchange with lane l^32.
+//     (16-byte LDS reads of K rows) and Q as the B operand (kept in VGPRs for
+//     the whole kernel).  In the accumulator a lane then holds one query column
+//     and 16 keys per 32x32 block, so the row max / sum are in-lane plus one
+//     exchange with lane l^32.
 //   * O^T = V^T P^T.  P^T comes straight from the S^T accumulators (converted
 //     to f16, no LDS round trip): accumulator rows 8c..8c+7 of a lane half are
-//     keys 16c + {0..3, 8..11} (+4 for the upper half), which is exactly the
-//     MFMA's k = 8*(l/32)+i if V^T is stored with the key positions inside each
-//     16-key group bit-2/bit-3 swapped.  V is transposed while it is staged
-//     into LDS, and its d rows are stored with the same swap so that every
-//     lane's O^T accumulators hold 8 contiguous head dims (16-byte stores).
-//   * K/V tiles are double-buffered in LDS: the next tile's global loads are
-//     issued before the current tile's MFMAs and written to the other buffer
-//     after them, one barrier per tile.  2 x 35 KB per workgroup, two
-//     workgroups per CU in the 160 KB LDS.
+//     keys 16c + {0..3, 8..11} (+4 for the upper half).  The V^T operand is
+//     read from the row-major V tile with ds_read_b64_tr_b16, which hands each
+//     lane 4 consecutive keys of one head dim; two such reads give the keys
+//     16c + 4h + {0..3} and 16c + 8 + 4h + {0..3} that line up with P's k.  The
+//     head dims a lane reads are permuted (bits 2/3 of d swapped) so that its
+//     O^T accumulators hold 8 contiguous head dims (16-byte output stores).
+//   * K and V tiles go from global memory straight into LDS
+//     (global_load_lds_dwordx4: no staging registers, no register transposes),
+//     double-buffered, one barrier per tile.  Rows are unpadded; 16-byte chunks
+//     are XOR-swizzled by row so that the K operand reads, the transposed V
+//     reads and the DMA writes are all free of bank conflicts.  32 KB per
+//     stage, 64 KB per workgroup, two workgroups per CU.
 //   * Causal: a workgroup processes query tile j and tile nqt-1-j, so every
 //     workgroup has the same amount of work; waves skip key tiles that lie
 //     entirely above their diagonal; masking runs only on diagonal/tail tiles.
@@ -32,7 +35,12 @@
 #include "attn_kernels.hpp"
 #include "wave.hpp"
 
+#define AK_LDS __attribute__((address_space(3)))
+#define AK_GLOBAL __attribute__((address_space(1)))
+
 namespace ak {
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 template <int D>
 struct PrefillTile {
@@ -40,74 +48,59 @@ struct PrefillTile {
     static constexpr int THREADS = NW * kWave;   // 256
     static constexpr int QW = 32;                // query rows per wave
     static constexpr int BM = NW * QW;           // query rows per workgroup
-    static constexpr int CH = D / 8;             // 16-byte chunks per K/V row
-    static constexpr int BN = 4 * THREADS / CH;  // keys per tile: 64 (D=128), 128 (D=64)
-    static constexpr int LDK = D + 8;            // K tile row stride (halves)
-    static constexpr int LDV = BN + 8;           // V^T tile row stride (halves)
-    static constexpr int K_ELEMS = BN * LDK;
-    static constexpr int V_ELEMS = D * LDV;
-    static constexpr int STAGE = K_ELEMS + V_ELEMS;  // halves per pipeline stage
+    static constexpr int CPR = D / 8;            // 16-byte chunks per K/V row
+    static constexpr int BN = 8192 / D;          // keys per tile (a K tile is 16 KB): 64 or 128
+    static constexpr int TILE = BN * D;          // halves per K (or V) tile
+    static constexpr int STAGE = 2 * TILE;       // K + V
+    static constexpr int RPI = 512 / D;          // rows per 1 KB load instruction
+    static constexpr int LPW = TILE * 2 / 1024 / NW;  // 1 KB load instructions per wave per tile
+    static constexpr int RPL = 128 / D;          // rows per 256-byte LDS bank line
     static constexpr int KB = BN / 32;           // 32-key blocks of S^T
     static constexpr int DC = D / 16;            // k-steps of K Q^T
     static constexpr int DT = D / 32;            // 32-row tiles of O^T
     static constexpr int PC = BN / 16;           // k-steps of V^T P^T
-    static constexpr int KLOADS = BN * CH / THREADS;  // 16-byte K loads per thread (4)
-    static constexpr int KG = BN / 4;            // groups of 4 keys in a tile (V staging)
-    static_assert(KLOADS == 4, "each thread stages 4 K chunks and 4 V rows per tile");
+    static_assert(LPW == 4, "each wave issues 4 one-KB loads per K and per V tile");
     static_assert(D % 32 == 0 && BN % 32 == 0, "tile shapes");
 };
 
+// Physical 16-byte chunk of logical chunk c in row r.  K: rows of one 256-byte
+// bank line sequence get distinct chunks, so 16 lanes reading one logical
+// chunk of 16 consecutive rows hit 16 different bank groups.  V: groups of 4
+// consecutive rows get disjoint 64-byte blocks, which is what one transposed
+// read of 4 rows x 16 head dims per 16 lanes needs.
 template <int D>
-struct Staged {
-    f16x8 k[PrefillTile<D>::KLOADS];
-    f16x8 v[4];
-};
+__device__ __forceinline__ int k_chunk(int r, int c) {
+    using T = PrefillTile<D>;
+    return c ^ ((r / T::RPL) % T::CPR);
+}
+template <int D>
+__device__ __forceinline__ int v_chunk(int r, int c) {
+    using T = PrefillTile<D>;
+    return c ^ (4 * ((r / T::RPL) % (T::CPR / 4)));
+}
 
-// Global -> registers for key tile [k0, k0 + BN).  Rows past n are clamped to
-// row n-1 instead of predicated: the loads stay branch-free and in bounds, and
-// the scores of those keys are masked to -inf, so their P is exactly 0.
+// Global -> LDS for key tile [k0, k0 + BN), asynchronous (vmcnt).  Each wave
+// writes 4 contiguous KB of each tile; lane l fills the 16-byte slot l of a KB.
+// Rows past n are clamped to row n-1: in bounds, and masked to -inf later.
 template <int D>
-__device__ __forceinline__ void stage_load(Staged<D>& st, const f16* __restrict__ kb,
-                                           const f16* __restrict__ vb, int k0, int n, int tid) {
+__device__ __forceinline__ void load_tile(const f16* __restrict__ kb, const f16* __restrict__ vb, f16* ks,
+                                          f16* vs, int k0, int n, int w, int lane) {
     using T = PrefillTile<D>;
 #pragma unroll
-    for (int j = 0; j < T::KLOADS; ++j) {
-        const int c = tid + j * T::THREADS;
-        const int row = c / T::CH, ch = c % T::CH;
-        const int key = min(k0 + row, n - 1);
-        st.k[j] = *reinterpret_cast<const f16x8*>(kb + (size_t)key * D + ch * 8);
-    }
-    const int kg = tid % T::KG, dc = tid / T::KG;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int key = min(k0 + kg * 4 + j, n - 1);
-        st.v[j] = *reinterpret_cast<const f16x8*>(vb + (size_t)key * D + dc * 8);
+    for (int j = 0; j < T::LPW; ++j) {
+        const int blk = w * T::LPW + j;
+        const int row = blk * T::RPI + lane / T::CPR, p = lane % T::CPR;
+        const size_t grow = (size_t)min(k0 + row, n - 1) * D;
+        __builtin_amdgcn_global_load_lds((AK_GLOBAL const void*)(kb + grow + k_chunk<D>(row, p) * 8),
+                                         (AK_LDS void*)(ks + blk * 512), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((AK_GLOBAL const void*)(vb + grow + v_chunk<D>(row, p) * 8),
+                                         (AK_LDS void*)(vs + blk * 512), 16, 0, 0);
     }
 }
 
-// Registers -> LDS stage: K row-major, V transposed with swapped key/d order.
-template <int D>
-__device__ __forceinline__ void stage_store(const Staged<D>& st, f16* __restrict__ ks,
-                                            f16* __restrict__ vs, int tid) {
-    using T = PrefillTile<D>;
-#pragma unroll
-    for (int j = 0; j < T::KLOADS; ++j) {
-        const int c = tid + j * T::THREADS;
-        const int row = c / T::CH, ch = c % T::CH;
-        *reinterpret_cast<f16x8*>(ks + row * T::LDK + ch * 8) = st.k[j];
-    }
-    // Lanes t..t+15 hold consecutive key groups of the same 8 head dims, so each
-    // 8-byte store instruction fills one whole V^T row: no bank conflicts.
-    const int kg = tid % T::KG, dc = tid / T::KG;
-    const int kl = kg * 4;                                  // first of 4 keys, multiple of 4
-    const int pos = (kl & ~15) | swap23(kl & 15);           // its slot in the V^T row
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const int d = dc * 8 + e;
-        const int lrow = (d & ~31) | swap23(d & 31);
-        const f16x4 col = {st.v[0][e], st.v[1][e], st.v[2][e], st.v[3][e]};
-        *reinterpret_cast<f16x4*>(vs + lrow * T::LDV + pos) = col;
-    }
+__device__ __forceinline__ void wait_loads_and_sync() {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
 }
 
 // {own value, value of lane l^32} in some order, by v_permlane32_swap on two
@@ -128,17 +121,6 @@ __device__ __forceinline__ float pair_sum(float x) {
     return v[0] + v[1];
 }
 
-// v *= a without moving v to new registers: as plain C++ the conditional
-// rescale below made the compiler copy all O accumulators on every tile.
-__device__ __forceinline__ void scale_in_place(f32x16& v, float a) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        float x = v[i];
-        asm volatile("v_mul_f32 %0, %0, %1" : "+v"(x) : "v"(a));
-        v[i] = x;
-    }
-}
-
 // The subtracted row maximum only moves when the tile's maximum exceeds it by
 // more than this many powers of two, so O is rescaled rarely.  Softmax is
 // invariant to the value subtracted; P stays <= 2^8, exact enough in fp16.
@@ -148,18 +130,21 @@ constexpr float kRescaleSlack = 8.f;
 template <int D, bool CAUSAL, bool MASK>
 __device__ __forceinline__ void tile_step(const f16* __restrict__ ks, const f16* __restrict__ vs,
                                           const f16x8 (&qf)[PrefillTile<D>::DC], f32x16 (&o)[PrefillTile<D>::DT],
-                                          float& ms_run, float& l_run, int k0, int n, int qrow, int col,
-                                          int half, float sl2) {
+                                          float& ms_run, float& l_run, int k0, int n, int qrow, int lane,
+                                          float sl2) {
     using T = PrefillTile<D>;
-    // S^T: KB blocks of 32 keys x 32 queries.
+    const int col = lane & 31, half = lane >> 5;
+    // S^T: KB blocks of 32 keys x 32 queries; lane reads key row 32b+col, chunk 2dc+half.
     f32x16 s[T::KB];
 #pragma unroll
     for (int b = 0; b < T::KB; ++b) {
         s[b] = f32x16{};
-        const f16* krow = ks + (b * 32 + col) * T::LDK + half * 8;
+        const int r = b * 32 + col;
+        const f16* krow = ks + r * D;
 #pragma unroll
         for (int dc = 0; dc < T::DC; ++dc)
-            s[b] = mfma32x32x16(*reinterpret_cast<const f16x8*>(krow + dc * 16), qf[dc], s[b]);
+            s[b] = mfma32x32x16(*reinterpret_cast<const f16x8*>(krow + k_chunk<D>(r, 2 * dc + half) * 8), qf[dc],
+                                s[b]);
     }
     if constexpr (MASK) {  // keys past n and, if causal, keys after the query
 #pragma unroll
@@ -205,13 +190,28 @@ __device__ __forceinline__ void tile_step(const f16* __restrict__ ks, const f16*
             ps[i] = __builtin_amdgcn_fdot2(f16x2{pf[c][2 * i], pf[c][2 * i + 1]}, ones, ps[i], false);
     }
     l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
-    // O^T += V^T P^T.
+
+    // O^T += V^T P^T.  Transposed reads: in each 16-lane group, lane a points at
+    // row kb + a/4, head dims dbase + 4*sw(a%4) (sw swaps bits 0/1); lane i then
+    // receives keys kb..kb+3 of head dim dbase + 4*sw(i/4) + i%4.
+    const int a = lane & 15, gd = (lane >> 4) & 1;
+    const int dsub = 16 * gd + 4 * (((a & 1) << 1) | ((a >> 1) & 1));  // within the 32-dim tile
 #pragma unroll
     for (int t = 0; t < T::DT; ++t) {
-        const f16* vrow = vs + (t * 32 + col) * T::LDV + half * 8;
+        const int dcol = t * 32 + dsub;
 #pragma unroll
-        for (int c = 0; c < T::PC; ++c)
-            o[t] = mfma32x32x16(*reinterpret_cast<const f16x8*>(vrow + c * 16), pf[c], o[t]);
+        for (int c = 0; c < T::PC; ++c) {
+            f16x4 lohi[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int r = 16 * c + 8 * e + 4 * half + (a >> 2);
+                const f16* p = vs + r * D + v_chunk<D>(r, dcol >> 3) * 8 + (dcol & 7);
+                lohi[e] = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((AK_LDS s16x4*)p));
+            }
+            const f16x8 va = {lohi[0][0], lohi[0][1], lohi[0][2], lohi[0][3],
+                              lohi[1][0], lohi[1][1], lohi[1][2], lohi[1][3]};
+            o[t] = mfma32x32x16(va, pf[c], o[t]);
+        }
     }
 }
 
@@ -226,6 +226,14 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
     const int col = lane & 31, half = lane >> 5;
     const int qw0 = q0 + w * T::QW;  // first query row of this wave
     const int qrow = qw0 + col;      // this lane's query row
+
+    const int kend = CAUSAL ? min(n, q0 + T::BM) : n;
+    const int nkt = (kend + T::BN - 1) / T::BN;
+    // Tiles before kt_mask need no masking for any wave of the workgroup: all
+    // their keys are < n and (causal) <= the workgroup's first query row.
+    const int kt_mask = min(nkt, CAUSAL ? q0 / T::BN : n / T::BN);
+
+    load_tile<D>(kb, vb, lds, lds + T::TILE, 0, n, w, lane);
 
     // Q as the MFMA B operand: col = query, k = head dim 16*dc + 8*half .. +7.
     f16x8 qf[T::DC];
@@ -246,43 +254,29 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
     float ms_run = -INFINITY; // the scaled row maximum subtracted so far
     float l_run = 0.f;        // this lane's share of the row sum
 
-    const int kend = CAUSAL ? min(n, q0 + T::BM) : n;
-    const int nkt = (kend + T::BN - 1) / T::BN;
-    // Tiles before kt_mask need no masking for any wave of the workgroup: all
-    // their keys are < n and (causal) <= the workgroup's first query row.
-    const int kt_mask = min(nkt, CAUSAL ? q0 / T::BN : n / T::BN);
-
-    Staged<D> st;
-    stage_load<D>(st, kb, vb, 0, n, tid);
-    stage_store<D>(st, lds, lds + T::K_ELEMS, tid);
-    __syncthreads();
+    wait_loads_and_sync();
 
     // Two loops with one tile body each (unmasked, then the diagonal/tail tiles
     // with masking), so that O stays in the same registers across iterations.
     for (int kt = 0; kt < kt_mask; ++kt) {
         f16* ks = lds + (kt & 1) * T::STAGE;
-        const bool more = kt + 1 < nkt;
-        if (more) stage_load<D>(st, kb, vb, (kt + 1) * T::BN, n, tid);
-        tile_step<D, CAUSAL, false>(ks, ks + T::K_ELEMS, qf, o, ms_run, l_run, kt * T::BN, n, qrow, col, half,
-                                    sl2);
-        if (more) {
+        if (kt + 1 < nkt) {
             f16* nks = lds + ((kt + 1) & 1) * T::STAGE;
-            stage_store<D>(st, nks, nks + T::K_ELEMS, tid);
+            load_tile<D>(kb, vb, nks, nks + T::TILE, (kt + 1) * T::BN, n, w, lane);
         }
-        __syncthreads();
+        tile_step<D, CAUSAL, false>(ks, ks + T::TILE, qf, o, ms_run, l_run, kt * T::BN, n, qrow, lane, sl2);
+        wait_loads_and_sync();
     }
     for (int kt = kt_mask; kt < nkt; ++kt) {
         const int k0 = kt * T::BN;
         f16* ks = lds + (kt & 1) * T::STAGE;
-        const bool more = kt + 1 < nkt;
-        if (more) stage_load<D>(st, kb, vb, k0 + T::BN, n, tid);
-        if (!CAUSAL || k0 <= qw0 + T::QW - 1)  // else every key of the tile is after this wave's rows
-            tile_step<D, CAUSAL, true>(ks, ks + T::K_ELEMS, qf, o, ms_run, l_run, k0, n, qrow, col, half, sl2);
-        if (more) {
+        if (kt + 1 < nkt) {
             f16* nks = lds + ((kt + 1) & 1) * T::STAGE;
-            stage_store<D>(st, nks, nks + T::K_ELEMS, tid);
+            load_tile<D>(kb, vb, nks, nks + T::TILE, k0 + T::BN, n, w, lane);
         }
-        __syncthreads();
+        if (!CAUSAL || k0 <= qw0 + T::QW - 1)  // else every key of the tile is after this wave's rows
+            tile_step<D, CAUSAL, true>(ks, ks + T::TILE, qf, o, ms_run, l_run, k0, n, qrow, lane, sl2);
+        wait_loads_and_sync();
     }
 
     // O = O^T / l.  Lane holds query qrow, head dims 32t + 16hh + 8*half + i.
@@ -308,7 +302,7 @@ flash_prefill_kernel(const f16* __restrict__ Q, const f16* __restrict__ K, const
                      f16* __restrict__ O, int n, int units_per_bh, int total_units, float sl2,
                      uint32_t qflip) {
     using T = PrefillTile<D>;
-    __shared__ __attribute__((aligned(16))) f16 lds[2 * T::STAGE];
+    __shared__ __attribute__((aligned(1024))) f16 lds[2 * T::STAGE];
     const int L = xcd_remap((int)blockIdx.x, total_units);
     const int bh = L / units_per_bh, u = L % units_per_bh;
     const size_t base = (size_t)bh * n * D;
@@ -317,10 +311,7 @@ flash_prefill_kernel(const f16* __restrict__ Q, const f16* __restrict__ K, const
         // Pair the heaviest remaining tile with the lightest: equal work per workgroup.
         const int heavy = nqt - 1 - u;
         prefill_qtile<D, true>(Q + base, K + base, V + base, O + base, lds, heavy * T::BM, n, sl2, qflip);
-        if (u != heavy) {
-            __syncthreads();
-            prefill_qtile<D, true>(Q + base, K + base, V + base, O + base, lds, u * T::BM, n, sl2, qflip);
-        }
+        if (u != heavy) prefill_qtile<D, true>(Q + base, K + base, V + base, O + base, lds, u * T::BM, n, sl2, qflip);
     } else {
         prefill_qtile<D, false>(Q + base, K + base, V + base, O + base, lds, u * T::BM, n, sl2, qflip);
     }
@@ -343,6 +334,5 @@ hipError_t prefill_launch(const PrefillArgs& a) {
     if (a.d == 64) return a.causal ? launch_prefill<64, true>(a) : launch_prefill<64, false>(a);
     return a.causal ? launch_prefill<128, true>(a) : launch_prefill<128, false>(a);
 }
-
 
 }  // namespace ak
