@@ -6,8 +6,11 @@
 // and guards, built for wave64 and the 32x32x16 matrix core instead of warps.
 //
 // Layout choices
-//   * A workgroup is 4 waves and owns BM = 128 query rows of one (batch, head);
+//   * A workgroup is 8 waves and owns BM = 256 query rows of one (batch, head);
 //     each wave owns 32 of them, so no softmax row is shared between waves.
+//     Eight waves share each K/V tile in LDS: half the LDS traffic per query
+//     row of a 4-wave workgroup, and each wave issues only 2 one-KB loads per
+//     K and per V tile.
 //   * Scores are computed transposed, S^T = K Q^T, with K as the MFMA A operand
 //     (16-byte LDS reads of K rows) and Q as the B operand (kept in VGPRs for
 //     the whole kernel).  In the accumulator a lane then holds one query column
@@ -26,7 +29,8 @@
 //     double-buffered, one barrier per tile.  Rows are unpadded; 16-byte chunks
 //     are XOR-swizzled by row so that the K operand reads, the transposed V
 //     reads and the DMA writes are all free of bank conflicts.  32 KB per
-//     stage, 64 KB per workgroup, two workgroups per CU.
+//     stage, 64 KB per workgroup.  At about 200 VGPRs a SIMD holds two waves,
+//     so a CU runs one 8-wave workgroup at a time.
 //   * Causal: a workgroup processes query tile j and tile nqt-1-j, so every
 //     workgroup has the same amount of work; waves skip key tiles that lie
 //     entirely above their diagonal; masking runs only on diagonal/tail tiles.
@@ -44,8 +48,8 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 template <int D>
 struct PrefillTile {
-    static constexpr int NW = 4;                 // waves per workgroup
-    static constexpr int THREADS = NW * kWave;   // 256
+    static constexpr int NW = 8;                 // waves per workgroup
+    static constexpr int THREADS = NW * kWave;   // 512
     static constexpr int QW = 32;                // query rows per wave
     static constexpr int BM = NW * QW;           // query rows per workgroup
     static constexpr int CPR = D / 8;            // 16-byte chunks per K/V row
@@ -59,7 +63,7 @@ struct PrefillTile {
     static constexpr int DC = D / 16;            // k-steps of K Q^T
     static constexpr int DT = D / 32;            // 32-row tiles of O^T
     static constexpr int PC = BN / 16;           // k-steps of V^T P^T
-    static_assert(LPW == 4, "each wave issues 4 one-KB loads per K and per V tile");
+    static_assert(LPW >= 1 && LPW * NW * 1024 == TILE * 2, "the waves split each tile into whole KBs");
     static_assert(D % 32 == 0 && BN % 32 == 0, "tile shapes");
 };
 
@@ -80,7 +84,7 @@ __device__ __forceinline__ int v_chunk(int r, int c) {
 }
 
 // Global -> LDS for key tile [k0, k0 + BN), asynchronous (vmcnt).  Each wave
-// writes 4 contiguous KB of each tile; lane l fills the 16-byte slot l of a KB.
+// writes LPW contiguous KB of each tile; lane l fills the 16-byte slot l of a KB.
 // Rows past n are clamped to row n-1: in bounds, and masked to -inf later.
 template <int D>
 __device__ __forceinline__ void load_tile(const f16* __restrict__ kb, const f16* __restrict__ vb, f16* ks,
@@ -297,7 +301,7 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
 }
 
 template <int D, bool CAUSAL>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ void __launch_bounds__(PrefillTile<D>::THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 flash_prefill_kernel(const f16* __restrict__ Q, const f16* __restrict__ K, const f16* __restrict__ V,
                      f16* __restrict__ O, int n, int units_per_bh, int total_units, float sl2,
                      uint32_t qflip) {
