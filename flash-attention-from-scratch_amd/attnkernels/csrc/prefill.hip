@@ -26,11 +26,16 @@
 //     O^T accumulators hold 8 contiguous head dims (16-byte output stores).
 //   * K and V tiles go from global memory straight into LDS
 //     (global_load_lds_dwordx4: no staging registers, no register transposes),
-//     double-buffered, one barrier per tile.  Rows are unpadded; 16-byte chunks
-//     are XOR-swizzled by row so that the K operand reads, the transposed V
-//     reads and the DMA writes are all free of bank conflicts.  32 KB per
-//     stage, 64 KB per workgroup.  At about 200 VGPRs a SIMD holds two waves,
-//     so a CU runs one 8-wave workgroup at a time.
+//     each in a ring of two tiles, one barrier per tile.  Rows are unpadded;
+//     16-byte chunks are XOR-swizzled by row so that the K operand reads, the
+//     transposed V reads and the DMA writes are all free of bank conflicts.
+//     64 KB per workgroup.  At about 230 VGPRs a SIMD holds two waves, so a CU
+//     runs one 8-wave workgroup at a time.
+//   * The key loop is software-pipelined inside each wave: while the matrix
+//     core computes the scores of tile t+1, the VALU turns the scores of tile
+//     t into P (exponentials, fp16 conversion, row sums), then P V of tile t
+//     follows.  sched_group_barrier fixes that interleave.  K is therefore
+//     loaded two tiles ahead and V one tile ahead.
 //   * Causal: a workgroup processes query tile j and tile nqt-1-j, so every
 //     workgroup has the same amount of work; waves skip key tiles that lie
 //     entirely above their diagonal; masking runs only on diagonal/tail tiles.
@@ -38,6 +43,8 @@
 //     run on the same XCD and share its L2.
 #include "attn_kernels.hpp"
 #include "wave.hpp"
+
+#include <type_traits>
 
 #define AK_LDS __attribute__((address_space(3)))
 #define AK_GLOBAL __attribute__((address_space(1)))
@@ -83,22 +90,20 @@ __device__ __forceinline__ int v_chunk(int r, int c) {
     return c ^ (4 * ((r / T::RPL) % (T::CPR / 4)));
 }
 
-// Global -> LDS for key tile [k0, k0 + BN), asynchronous (vmcnt).  Each wave
-// writes LPW contiguous KB of each tile; lane l fills the 16-byte slot l of a KB.
-// Rows past n are clamped to row n-1: in bounds, and masked to -inf later.
-template <int D>
-__device__ __forceinline__ void load_tile(const f16* __restrict__ kb, const f16* __restrict__ vb, f16* ks,
-                                          f16* vs, int k0, int n, int w, int lane) {
+// Global -> LDS for one K (or V) tile, keys [k0, k0 + BN), asynchronous
+// (vmcnt).  Each wave writes LPW contiguous KB of the tile; lane l fills the
+// 16-byte slot l of a KB.  Rows past n are clamped to row n-1: in bounds, and
+// masked to -inf later.
+template <int D, bool IS_V>
+__device__ __forceinline__ void load_kv(const f16* __restrict__ src, f16* dst, int k0, int n, int w, int lane) {
     using T = PrefillTile<D>;
 #pragma unroll
     for (int j = 0; j < T::LPW; ++j) {
         const int blk = w * T::LPW + j;
         const int row = blk * T::RPI + lane / T::CPR, p = lane % T::CPR;
-        const size_t grow = (size_t)min(k0 + row, n - 1) * D;
-        __builtin_amdgcn_global_load_lds((AK_GLOBAL const void*)(kb + grow + k_chunk<D>(row, p) * 8),
-                                         (AK_LDS void*)(ks + blk * 512), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((AK_GLOBAL const void*)(vb + grow + v_chunk<D>(row, p) * 8),
-                                         (AK_LDS void*)(vs + blk * 512), 16, 0, 0);
+        const int c = IS_V ? v_chunk<D>(row, p) : k_chunk<D>(row, p);
+        __builtin_amdgcn_global_load_lds((AK_GLOBAL const void*)(src + (size_t)min(k0 + row, n - 1) * D + c * 8),
+                                         (AK_LDS void*)(dst + blk * 512), 16, 0, 0);
     }
 }
 
@@ -130,16 +135,13 @@ __device__ __forceinline__ float pair_sum(float x) {
 // invariant to the value subtracted; P stays <= 2^8, exact enough in fp16.
 constexpr float kRescaleSlack = 8.f;
 
-// One key tile for one wave: S^T = K Q^T, online softmax, O^T += V^T P^T.
-template <int D, bool CAUSAL, bool MASK>
-__device__ __forceinline__ void tile_step(const f16* __restrict__ ks, const f16* __restrict__ vs,
-                                          const f16x8 (&qf)[PrefillTile<D>::DC], f32x16 (&o)[PrefillTile<D>::DT],
-                                          float& ms_run, float& l_run, int k0, int n, int qrow, int lane,
-                                          float sl2) {
+// S^T = K Q^T for one key tile: KB blocks of 32 keys x 32 queries; lane reads
+// key row 32b+col, chunk 2dc+half.
+template <int D>
+__device__ __forceinline__ void qk_tile(const f16* __restrict__ ks, const f16x8 (&qf)[PrefillTile<D>::DC],
+                                        f32x16 (&s)[PrefillTile<D>::KB], int lane) {
     using T = PrefillTile<D>;
     const int col = lane & 31, half = lane >> 5;
-    // S^T: KB blocks of 32 keys x 32 queries; lane reads key row 32b+col, chunk 2dc+half.
-    f32x16 s[T::KB];
 #pragma unroll
     for (int b = 0; b < T::KB; ++b) {
         s[b] = f32x16{};
@@ -150,15 +152,27 @@ __device__ __forceinline__ void tile_step(const f16* __restrict__ ks, const f16*
             s[b] = mfma32x32x16(*reinterpret_cast<const f16x8*>(krow + k_chunk<D>(r, 2 * dc + half) * 8), qf[dc],
                                 s[b]);
     }
-    if constexpr (MASK) {  // keys past n and, if causal, keys after the query
+}
+
+// Keys past n and, if causal, keys after the query -> -inf.
+template <int D, bool CAUSAL>
+__device__ __forceinline__ void mask_tile(f32x16 (&s)[PrefillTile<D>::KB], int k0, int n, int qrow, int half) {
+    using T = PrefillTile<D>;
 #pragma unroll
-        for (int b = 0; b < T::KB; ++b)
+    for (int b = 0; b < T::KB; ++b)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = k0 + b * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-                if (key >= n || (CAUSAL && key > qrow)) s[b][r] = -INFINITY;
-            }
-    }
+        for (int r = 0; r < 16; ++r) {
+            const int key = k0 + b * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+            if (key >= n || (CAUSAL && key > qrow)) s[b][r] = -INFINITY;
+        }
+}
+
+// Tile row maximum; moves the subtracted maximum (and rescales O and l) only
+// when it grows by more than kRescaleSlack, which is rare after the first tile.
+template <int D>
+__device__ __forceinline__ void max_tile(const f32x16 (&s)[PrefillTile<D>::KB], f32x16 (&o)[PrefillTile<D>::DT],
+                                         float& ms_run, float& l_run, float sl2) {
+    using T = PrefillTile<D>;
     float mx = -INFINITY;
 #pragma unroll
     for (int b = 0; b < T::KB; ++b)
@@ -166,7 +180,7 @@ __device__ __forceinline__ void tile_step(const f16* __restrict__ ks, const f16*
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
     const float mxs = pair_max(mx) * sl2;  // this tile's scaled row max (-inf if all masked)
     const bool grow = mxs > ms_run + kRescaleSlack;  // always true on the first tile
-    if (__builtin_amdgcn_ballot_w64(grow)) {          // rare after the first tile
+    if (__builtin_amdgcn_ballot_w64(grow)) {
         const float ms_new = grow ? mxs : ms_run;
         const float alpha = exp2_fast(ms_run - ms_new);  // 0 on the first tile, 1 if unchanged
         ms_run = ms_new;
@@ -174,31 +188,36 @@ __device__ __forceinline__ void tile_step(const f16* __restrict__ ks, const f16*
 #pragma unroll
         for (int t = 0; t < T::DT; ++t) o[t] *= alpha;
     }
-#pragma unroll
-    for (int b = 0; b < T::KB; ++b)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[b][r] = exp2_fast(fmaf(s[b][r], sl2, -ms_run));  // masked: 2^-inf = 0
+}
 
-    // P^T as the B operand: k-step c = accumulator regs 8*(c%2).. of block c/2.
-    // The row sum is taken over the same fp16 values the MFMA consumes, two at
-    // a time by v_dot2_f32_f16 against (1, 1), in 4 independent chains.
-    f16x8 pf[T::PC];
+// P^T = 2^(S^T sl2 - ms) as the fp16 B operand: k-step c = accumulator regs
+// 8*(c%2).. of block c/2.  The row sum is taken over the same fp16 values the
+// MFMA consumes, two at a time by v_dot2_f32_f16 against (1, 1), in 4 chains.
+template <int D>
+__device__ __forceinline__ void exp_tile(const f32x16 (&s)[PrefillTile<D>::KB], f16x8 (&pf)[PrefillTile<D>::PC],
+                                         float ms_run, float& l_run, float sl2) {
+    using T = PrefillTile<D>;
     float ps[4] = {0.f, 0.f, 0.f, 0.f};
     const f16x2 ones = {(f16)1.f, (f16)1.f};
 #pragma unroll
     for (int c = 0; c < T::PC; ++c) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) pf[c][i] = (f16)s[c >> 1][(c & 1) * 8 + i];
+        for (int i = 0; i < 8; ++i) pf[c][i] = (f16)exp2_fast(fmaf(s[c >> 1][(c & 1) * 8 + i], sl2, -ms_run));
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             ps[i] = __builtin_amdgcn_fdot2(f16x2{pf[c][2 * i], pf[c][2 * i + 1]}, ones, ps[i], false);
     }
     l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+}
 
-    // O^T += V^T P^T.  Transposed reads: in each 16-lane group, lane a points at
-    // row kb + a/4, head dims dbase + 4*sw(a%4) (sw swaps bits 0/1); lane i then
-    // receives keys kb..kb+3 of head dim dbase + 4*sw(i/4) + i%4.
-    const int a = lane & 15, gd = (lane >> 4) & 1;
+// O^T += V^T P^T.  Transposed reads: in each 16-lane group, lane a points at
+// row kb + a/4, head dims dbase + 4*sw(a%4) (sw swaps bits 0/1); lane i then
+// receives keys kb..kb+3 of head dim dbase + 4*sw(i/4) + i%4.
+template <int D>
+__device__ __forceinline__ void pv_tile(const f16* __restrict__ vs, const f16x8 (&pf)[PrefillTile<D>::PC],
+                                        f32x16 (&o)[PrefillTile<D>::DT], int lane) {
+    using T = PrefillTile<D>;
+    const int half = lane >> 5, a = lane & 15, gd = (lane >> 4) & 1;
     const int dsub = 16 * gd + 4 * (((a & 1) << 1) | ((a >> 1) & 1));  // within the 32-dim tile
 #pragma unroll
     for (int t = 0; t < T::DT; ++t) {
@@ -219,6 +238,17 @@ __device__ __forceinline__ void tile_step(const f16* __restrict__ ks, const f16*
     }
 }
 
+// Instruction interleave of one pipelined tile (sched_group_barrier masks:
+// 0x008 MFMA, 0x002 VALU, 0x400 transcendental, 0x100 LDS read).  Per MFMA of
+// the next tile's S: a few VALU ops and exponentials of this tile's P and the
+// K read for a later MFMA; K reads run kKPrefetch ahead, V reads kVPrefetch.
+constexpr int kValuPerMfma = 3, kExpPerMfma = 2, kKPrefetch = 2, kVPrefetch = 4;
+
+// Software-pipelined key loop: iteration t multiplies the scores of tile t
+// (computed one iteration earlier) into O while the matrix core computes the
+// scores of tile t+1, so the exponentials of one tile overlap the QK^T MFMAs
+// of the next inside every wave.  K runs two tiles ahead in a 2-buffer ring,
+// V one tile ahead in another; one barrier per tile.
 template <int D, bool CAUSAL>
 __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const f16* __restrict__ kb,
                                               const f16* __restrict__ vb, f16* __restrict__ ob,
@@ -228,8 +258,10 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = uniform(tid >> 6);
     const int col = lane & 31, half = lane >> 5;
-    const int qw0 = q0 + w * T::QW;  // first query row of this wave
-    const int qrow = qw0 + col;      // this lane's query row
+    const int qw0 = q0 + w * T::QW;
+    const int qrow = qw0 + col;
+    f16* kbuf = lds;                 // 2 K tiles
+    f16* vbuf = lds + 2 * T::TILE;   // 2 V tiles
 
     const int kend = CAUSAL ? min(n, q0 + T::BM) : n;
     const int nkt = (kend + T::BN - 1) / T::BN;
@@ -237,7 +269,9 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
     // their keys are < n and (causal) <= the workgroup's first query row.
     const int kt_mask = min(nkt, CAUSAL ? q0 / T::BN : n / T::BN);
 
-    load_tile<D>(kb, vb, lds, lds + T::TILE, 0, n, w, lane);
+    load_kv<D, false>(kb, kbuf, 0, n, w, lane);
+    load_kv<D, true>(vb, vbuf, 0, n, w, lane);
+    if (nkt > 1) load_kv<D, false>(kb, kbuf + T::TILE, T::BN, n, w, lane);
 
     // Q as the MFMA B operand: col = query, k = head dim 16*dc + 8*half .. +7.
     f16x8 qf[T::DC];
@@ -251,7 +285,6 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
         }
         qf[dc] = x;
     }
-
     f32x16 o[T::DT];
 #pragma unroll
     for (int t = 0; t < T::DT; ++t) o[t] = f32x16{};
@@ -259,28 +292,59 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
     float l_run = 0.f;        // this lane's share of the row sum
 
     wait_loads_and_sync();
+    // S(t) alternates between sx and sy (loop unrolled by 2: no copies).
+    f32x16 sx[T::KB], sy[T::KB];
+    qk_tile<D>(kbuf, qf, sx, lane);
 
-    // Two loops with one tile body each (unmasked, then the diagonal/tail tiles
-    // with masking), so that O stays in the same registers across iterations.
-    for (int kt = 0; kt < kt_mask; ++kt) {
-        f16* ks = lds + (kt & 1) * T::STAGE;
-        if (kt + 1 < nkt) {
-            f16* nks = lds + ((kt + 1) & 1) * T::STAGE;
-            load_tile<D>(kb, vb, nks, nks + T::TILE, (kt + 1) * T::BN, n, w, lane);
+    // One tile: sc holds S(t); sn receives S(t+1).  Past the last tile the
+    // next K buffer holds stale (in-bounds) data; that S is never used.
+    auto body = [&](int t, f32x16 (&sc)[T::KB], f32x16 (&sn)[T::KB], auto mask_tag) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        wait_loads_and_sync();  // K(t+1), V(t) landed; nobody reads K(t), V(t-1) any more
+        if (t + 2 < nkt) load_kv<D, false>(kb, kbuf + (t & 1) * T::TILE, (t + 2) * T::BN, n, w, lane);
+        if (t + 1 < nkt) load_kv<D, true>(vb, vbuf + ((t + 1) & 1) * T::TILE, (t + 1) * T::BN, n, w, lane);
+        // Causal: a tile whose first key is after this wave's last row is skipped.
+        const bool act = !MASK || !CAUSAL || t * T::BN <= qw0 + T::QW - 1;
+        if (act) {
+            if constexpr (MASK) mask_tile<D, CAUSAL>(sc, t * T::BN, n, qrow, half);
+            max_tile<D>(sc, o, ms_run, l_run, sl2);
         }
-        tile_step<D, CAUSAL, false>(ks, ks + T::TILE, qf, o, ms_run, l_run, kt * T::BN, n, qrow, lane, sl2);
-        wait_loads_and_sync();
+        qk_tile<D>(kbuf + ((t + 1) & 1) * T::TILE, qf, sn, lane);
+        if (act) {
+            f16x8 pf[T::PC];
+            exp_tile<D>(sc, pf, ms_run, l_run, sl2);
+            pv_tile<D>(vbuf + (t & 1) * T::TILE, pf, o, lane);
+            __builtin_amdgcn_sched_group_barrier(0x100, kKPrefetch, 0);
+#pragma unroll
+            for (int i = 0; i < T::KB * T::DC; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (S of the next tile)
+                __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);  // VALU (this tile's P)
+                __builtin_amdgcn_sched_group_barrier(0x400, kExpPerMfma, 0);  // exp
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // next K fragment read
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, kVPrefetch, 0);
+#pragma unroll
+            for (int i = 0; i < T::DT * T::PC; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (O += V^T P^T)
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // transposed V reads
+            }
+        }
+    };
+    int t = 0;
+    for (; t + 1 < kt_mask; t += 2) {
+        body(t, sx, sy, std::false_type{});
+        body(t + 1, sy, sx, std::false_type{});
     }
-    for (int kt = kt_mask; kt < nkt; ++kt) {
-        const int k0 = kt * T::BN;
-        f16* ks = lds + (kt & 1) * T::STAGE;
-        if (kt + 1 < nkt) {
-            f16* nks = lds + ((kt + 1) & 1) * T::STAGE;
-            load_tile<D>(kb, vb, nks, nks + T::TILE, k0 + T::BN, n, w, lane);
-        }
-        if (!CAUSAL || k0 <= qw0 + T::QW - 1)  // else every key of the tile is after this wave's rows
-            tile_step<D, CAUSAL, true>(ks, ks + T::TILE, qf, o, ms_run, l_run, k0, n, qrow, lane, sl2);
-        wait_loads_and_sync();
+    if (t < kt_mask) {
+        body(t, sx, sy, std::false_type{});
+#pragma unroll
+        for (int b = 0; b < T::KB; ++b) sx[b] = sy[b];
+        ++t;
+    }
+    for (; t < nkt; ++t) {
+        body(t, sx, sy, std::true_type{});
+#pragma unroll
+        for (int b = 0; b < T::KB; ++b) sx[b] = sy[b];
     }
 
     // O = O^T / l.  Lane holds query qrow, head dims 32t + 16hh + 8*half + i.
@@ -289,13 +353,13 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
     if (qrow < n) {
         f16* orow = ob + (size_t)qrow * D + half * 8;
 #pragma unroll
-        for (int t = 0; t < T::DT; ++t)
+        for (int t2 = 0; t2 < T::DT; ++t2)
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
                 f16x8 v;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) v[i] = (f16)(o[t][hh * 8 + i] * inv);
-                *reinterpret_cast<f16x8*>(orow + t * 32 + hh * 16) = v;
+                for (int i = 0; i < 8; ++i) v[i] = (f16)(o[t2][hh * 8 + i] * inv);
+                *reinterpret_cast<f16x8*>(orow + t2 * 32 + hh * 16) = v;
             }
     }
 }
@@ -315,7 +379,10 @@ flash_prefill_kernel(const f16* __restrict__ Q, const f16* __restrict__ K, const
         // Pair the heaviest remaining tile with the lightest: equal work per workgroup.
         const int heavy = nqt - 1 - u;
         prefill_qtile<D, true>(Q + base, K + base, V + base, O + base, lds, heavy * T::BM, n, sl2, qflip);
-        if (u != heavy) prefill_qtile<D, true>(Q + base, K + base, V + base, O + base, lds, u * T::BM, n, sl2, qflip);
+        if (u != heavy) {
+            __syncthreads();  // every wave is done with the buffers before they are refilled
+            prefill_qtile<D, true>(Q + base, K + base, V + base, O + base, lds, u * T::BM, n, sl2, qflip);
+        }
     } else {
         prefill_qtile<D, false>(Q + base, K + base, V + base, O + base, lds, u * T::BM, n, sl2, qflip);
     }
