@@ -98,13 +98,27 @@ def _sm_count(device_index):
     return torch.cuda.get_device_properties(device_index).multi_processor_count
 
 
-def decode_partition(batch, num_kv_heads, max_context_len, device=None):
-    """Tokens per split for paged_decode: enough splits for about 4 workgroups
-    per CU in total, at least one 256-token chunk per split
-    (reference attnkernels/__init__.py:93-101)."""
+# Split-count target of decode_partition, in decode workgroups per compute
+# unit.  The reference's rule aims at 4 blocks per SM (attnkernels/__init__.py:
+# 94-98, tuned on a T4).  The partition is chosen from max_context_len alone
+# (reading the lengths would cost a host sync), so the rule must hold for
+# uniform and for mixed-length batches.  In the MI355X split-K ablation of
+# ``attnkernels.benchsuite`` (every power-of-two partition; 5 uniform and 3
+# mixed-length batches, Hkv=8) a target of 16 per CU reaches >= 92% of the best
+# partition in every case; 4 drops to 75% and 2 to 66% on mixed lengths, where
+# too few splits leave the longest sequences as a tail (results/mi355x.md).
+DECODE_WG_PER_CU = 16
+REFERENCE_WG_PER_SM = 4
+
+
+def decode_partition(batch, num_kv_heads, max_context_len, device=None, wg_per_cu=DECODE_WG_PER_CU):
+    """Tokens per split for paged_decode: enough splits for about ``wg_per_cu``
+    workgroups per CU in total, at least one 256-token chunk per split
+    (reference attnkernels/__init__.py:93-101, whose rule is
+    ``wg_per_cu=REFERENCE_WG_PER_SM``)."""
     dev = torch.cuda.current_device() if device is None else device
     blocks = batch * num_kv_heads
-    want = -(-4 * _sm_count(dev) // blocks)
+    want = -(-int(wg_per_cu) * _sm_count(dev) // blocks)
     max_chunks = -(-max_context_len // CHUNK)
     splits = max(1, min(want, max_chunks))
     return -(-max_chunks // splits) * CHUNK

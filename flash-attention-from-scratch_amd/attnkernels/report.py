@@ -1,0 +1,133 @@
+"""Markdown report of a ``benchsuite`` JSON file (the counterpart of the
+reference's bench/report.py:36-98): device and ceilings, then one table per
+section, with this build's kernels as fractions of the MI355X peaks.
+
+    python -m attnkernels.report results/mi355x.json > results/mi355x.md
+"""
+from __future__ import annotations
+
+import json
+import sys
+from collections import defaultdict
+
+PEAK_TFLOPS = 2500.0  # dense fp16 MFMA
+PEAK_GBS = 8000.0     # HBM3E
+
+
+def _table(header, rows):
+    out = ["| " + " | ".join(header) + " |", "|" + "---|" * len(header)]
+    out += ["| " + " | ".join(str(c) for c in r) + " |" for r in rows]
+    return "\n".join(out)
+
+
+def prefill_tables(rows):
+    impls = []
+    for r in rows:
+        if r["impl"] not in impls:
+            impls.append(r["impl"])
+    parts = []
+    for d in (64, 128):
+        for causal in (False, True):
+            sel = [r for r in rows if r["head_dim"] == d and r["causal"] == causal]
+            if not sel:
+                continue
+            by_n = defaultdict(dict)
+            for r in sel:
+                by_n[(r["batch"], r["seq"])][r["impl"]] = r
+            body = []
+            for (b, n), rs in sorted(by_n.items(), key=lambda kv: kv[0][1]):
+                cells = [f"{b}x{n}"]
+                for i in impls:
+                    r = rs.get(i)
+                    cells.append(f"{r['tflops']:.1f}" if r else "-")
+                ours = rs.get("flash_attention")
+                cells.append(f"{100 * ours['tflops'] / PEAK_TFLOPS:.1f}%" if ours else "-")
+                cells.append(f"{ours['speedup_vs_sdpa']}x" if ours and ours.get("speedup_vs_sdpa") else "-")
+                cells.append(f"{ours['max_abs_err']:.1e}" if ours else "-")
+                body.append(cells)
+            parts.append(f"**D={d}, {'causal' if causal else 'non-causal'}** (TFLOP/s; H=16)\n\n" +
+                         _table(["B x N"] + impls + ["flash % peak", "vs SDPA", "max err"], body))
+    return "\n\n".join(parts)
+
+
+def decode_table(rows, section):
+    sel = [r for r in rows if r["section"] == section]
+    if not sel:
+        return ""
+    impls = []
+    for r in sel:
+        if r["impl"] not in impls:
+            impls.append(r["impl"])
+    by_case = defaultdict(dict)
+    for r in sel:
+        by_case[(r["batch"], r["ctx"])][r["impl"]] = r
+    body = []
+    for (b, c), rs in sorted(by_case.items()):
+        cells = [b, c]
+        for i in impls:
+            r = rs.get(i)
+            cells.append(f"{r['gbs']:.0f}" if r else "-")
+        ours = rs.get("paged_split")
+        cells.append(f"{100 * ours['gbs'] / PEAK_GBS:.1f}%" if ours else "-")
+        cells.append(ours.get("partition", "-") if ours else "-")
+        cells.append(f"{ours['speedup_vs_torch_gather']}x" if ours and ours.get("speedup_vs_torch_gather") else "-")
+        body.append(cells)
+    return _table(["B", "max ctx"] + [f"{i} GB/s" for i in impls] + ["split % HBM", "P", "vs gather+SDPA"], body)
+
+
+def ablation_table(rows, section="split_ablation"):
+    sel = [r for r in rows if r["section"] == section]
+    if not sel:
+        return ""
+    by_case = defaultdict(list)
+    for r in sel:
+        by_case[(r["batch"], r["ctx"])].append(r)
+    body = []
+    for (b, c), rs in sorted(by_case.items()):
+        best = max(rs, key=lambda r: r["gbs"])
+        curve = ", ".join(f"{r['partition']}:{r['gbs']:.0f}" for r in sorted(rs, key=lambda r: r["partition"]))
+        body.append([b, c, best["partition"], f"{best['gbs']:.0f}", curve])
+    return _table(["B", "ctx", "best P", "best GB/s", "P:GB/s"], body)
+
+
+def render(data):
+    meta, rows = data["meta"], data["results"]
+    lines = [f"# Attention kernels on {meta.get('gpu')} ({meta.get('arch')}, {meta.get('cu_count')} CUs)", ""]
+    lines.append(f"torch {meta.get('torch')}, HIP {meta.get('hip')}, {meta.get('date')}.  "
+                 f"Timing: {meta.get('timing')}.")
+    roofs = meta.get("roofs", {})
+    lines += ["", f"Ceilings measured here: device copy {roofs.get('copy_gbs')} GB/s "
+                  f"({100 * roofs.get('copy_gbs', 0) / PEAK_GBS:.0f}% of 8 TB/s), fp16 GEMM 8192^3 "
+                  f"{roofs.get('fp16_gemm_tflops')} TFLOP/s ({100 * roofs.get('fp16_gemm_tflops', 0) / PEAK_TFLOPS:.0f}% "
+                  f"of 2.5 PFLOP/s).", ""]
+    lines.append("SDPA backends: " + ", ".join(f"{k}: {v}" for k, v in meta.get("sdpa_backends", {}).items()))
+    pre = [r for r in rows if r["section"] == "prefill"]
+    if pre:
+        lines += ["", "## Prefill", "", prefill_tables(pre)]
+    for section, title in (("decode", "Paged decode (Hq=32, Hkv=8, D=128, page 16)"),
+                           ("ragged", "Ragged batch")):
+        t = decode_table(rows, section)
+        if t:
+            lines += ["", f"## {title}", "", t]
+    t = ablation_table(rows)
+    if t:
+        lines += ["", "## Split-K partition ablation", "", t]
+    t = ablation_table(rows, "split_ablation_ragged")
+    if t:
+        lines += ["", "## Split-K partition ablation, mixed context lengths (ctx = max)", "", t]
+    if meta.get("failed_sections"):
+        lines += ["", "Failed sections: " + json.dumps(meta["failed_sections"])]
+    return "\n".join(lines) + "\n"
+
+
+def main(argv=None):
+    argv = sys.argv[1:] if argv is None else argv
+    if len(argv) != 1:
+        raise SystemExit("usage: python -m attnkernels.report results.json")
+    with open(argv[0]) as f:
+        sys.stdout.write(render(json.load(f)))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

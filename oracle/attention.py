@@ -66,14 +66,14 @@ def decode_kv_bytes(context_lens, num_kv_heads, head_dim):
     return int(sum(int(c) for c in context_lens)) * num_kv_heads * head_dim * 2 * 2
 
 
-def decode_partition(batch, num_kv_heads, max_context_len, sm_count):
+def decode_partition(batch, num_kv_heads, max_context_len, sm_count, wg_per_sm=4):
     """Tokens per split, attnkernels/__init__.py:93-101.
 
-    want = ceil(4*SMs / (B*Hkv)); splits = clamp(want, 1, ceil(max_ctx/256));
-    partition = ceil(chunks/splits)*256.
+    want = ceil(wg_per_sm*SMs / (B*Hkv)); splits = clamp(want, 1, ceil(max_ctx/256));
+    partition = ceil(chunks/splits)*256.  The reference's factor is 4.
     """
     blocks = batch * num_kv_heads
-    want = -(-4 * sm_count // blocks)
+    want = -(-wg_per_sm * sm_count // blocks)
     max_chunks = -(-max_context_len // CHUNK)
     splits = max(1, min(want, max_chunks))
     return -(-max_chunks // splits) * CHUNK

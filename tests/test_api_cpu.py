@@ -49,14 +49,36 @@ def test_decode_partition_matches_reference_t4_run(monkeypatch):
     fx = json.loads((GOLDEN / "decode_partition_t4.json").read_text())
     monkeypatch.setattr(ak, "_sm_count", lambda dev: fx["sm_count"])
     for r in fx["rows"]:
-        assert ak.decode_partition(r["batch"], r["num_kv_heads"], r["max_context_len"], 0) == \
-            r["partition"], r
+        assert ak.decode_partition(r["batch"], r["num_kv_heads"], r["max_context_len"], 0,
+                                   wg_per_cu=ak.REFERENCE_WG_PER_SM) == r["partition"], r
 
 
 def test_decode_partition_on_256_cus(monkeypatch):
     monkeypatch.setattr(ak, "_sm_count", lambda dev: 256)
     for b, hkv, ctx in [(64, 32, 4096), (8, 32, 32768), (1, 8, 32768), (3, 8, 1)]:
-        assert ak.decode_partition(b, hkv, ctx, 0) == oracle.decode_partition(b, hkv, ctx, 256)
+        assert ak.decode_partition(b, hkv, ctx, 0) == \
+            oracle.decode_partition(b, hkv, ctx, 256, wg_per_sm=ak.DECODE_WG_PER_CU)
+        assert ak.decode_partition(b, hkv, ctx, 0, wg_per_cu=4) == oracle.decode_partition(b, hkv, ctx, 256)
+
+
+def test_decode_partition_default_is_near_the_measured_optimum(monkeypatch):
+    """On 256 CUs the default rule picks a partition within 12% of the fastest
+    one in every case of the MI355X split-K ablation, uniform and mixed context
+    lengths (tests/golden/decode_partition_mi355x.json: bandwidth of every
+    power-of-two partition per case); the reference's factor does not."""
+    fx = json.loads((GOLDEN / "decode_partition_mi355x.json").read_text())
+    monkeypatch.setattr(ak, "_sm_count", lambda dev: fx["cu_count"])
+    assert fx["rows"] and any(r["mixed_lengths"] for r in fx["rows"])
+
+    def worst(factor):
+        fr = []
+        for r in fx["rows"]:
+            p = ak.decode_partition(r["batch"], r["num_kv_heads"], r["max_context_len"], 0, wg_per_cu=factor)
+            fr.append(r["gbs"][str(p)] / max(r["gbs"].values()))
+        return min(fr)
+
+    assert worst(ak.DECODE_WG_PER_CU) >= 0.88
+    assert worst(ak.REFERENCE_WG_PER_SM) < worst(ak.DECODE_WG_PER_CU)
 
 
 def test_reference_module_attention_matches_oracle():

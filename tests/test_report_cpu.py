@@ -1,0 +1,45 @@
+"""CPU checks of the comparison-suite report (attnkernels.report) on a small
+synthetic results file, and of the committed MI355X results."""
+import json
+from pathlib import Path
+
+from attnkernels import report
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _rows():
+    rows = []
+    for impl, ms in (("flash_attention", 0.5), ("sdpa_fused", 1.0)):
+        rows.append(dict(section="prefill", impl=impl, batch=2, heads=16, seq=8192, head_dim=128, causal=True,
+                         ms=ms, tflops=2200.0 / ms / 2, peak_mem_mb=64.0, max_abs_err=5e-4,
+                         speedup_vs_sdpa=1.0 / ms))
+    for p, gbs in ((256, 3000.0), (512, 3600.0), (1024, 3100.0)):
+        rows.append(dict(section="split_ablation", impl="paged_split", batch=1, ctx=4096, kv_heads=8,
+                         partition=p, gbs=gbs, ms=1.0, max_abs_err=1e-5))
+    rows.append(dict(section="decode", impl="paged_split", batch=4, ctx=4096, partition=512, gbs=4000.0,
+                     ms=0.1, max_abs_err=1e-5, speedup_vs_torch_gather=5.0))
+    rows.append(dict(section="decode", impl="torch_gather_sdpa", batch=4, ctx=4096, gbs=800.0, ms=0.5,
+                     max_abs_err=1e-5, speedup_vs_torch_gather=1.0))
+    return rows
+
+
+def test_render_synthetic():
+    meta = dict(gpu="MI355X", arch="gfx950", cu_count=256, torch="x", hip="y", date="d", timing="t",
+                roofs=dict(copy_gbs=4000.0, fp16_gemm_tflops=1250.0), sdpa_backends={"FLASH_ATTENTION": "ok"})
+    md = report.render(dict(meta=meta, results=_rows()))
+    assert "## Prefill" in md and "## Paged decode" in md and "## Split-K partition ablation" in md
+    assert "| 2x8192 | 2200.0 | 1100.0 | 88.0% | 2.0x | 5.0e-04 |" in md
+    assert "| 1 | 4096 | 512 | 3600 |" in md  # best partition of the ablation
+    assert "| 4 | 4096 | 4000 | 800 | 50.0% | 512 | 5.0x |" in md
+    assert "50% of 8 TB/s" in md and "50% of 2.5 PFLOP/s" in md
+
+
+def test_committed_results_render():
+    data = json.loads((ROOT / "results" / "mi355x.json").read_text())
+    md = report.render(data)
+    assert md.startswith("# Attention kernels on")
+    ours = [r for r in data["results"] if r["section"] == "prefill" and r["impl"] == "flash_attention"]
+    assert ours and all(r["max_abs_err"] < 4e-3 for r in ours)
+    dec = [r for r in data["results"] if r["impl"] == "paged_split"]
+    assert dec and all(r["max_abs_err"] < 2e-3 for r in dec)
