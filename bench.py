@@ -8,9 +8,10 @@ the reference's FLOP convention 4*B*H*N^2*D/2 (bench/bench.py:153).  A step is
 one prefill call over that batch with inputs already resident in HBM.
 
 The same line carries, under ``workloads``, the other BASELINE configs measured
-the same way: non-causal prefill, the N=8191 variant, and the two
+the same way: non-causal prefill, the N=8191 variant, the two
 paged split-K decode configs in KV GB/s with the reference's byte convention
-sum(ctx)*Hkv*D*2*2 (bench/bench.py:199-200).
+sum(ctx)*Hkv*D*2*2 (bench/bench.py:199-200), and the paged cache writer
+(K/V rows read + written, GB/s).
 
 ``roofline`` is the headline kernel's algorithmic FLOP per launch divided by its
 mean launch duration (HIP events on the launch stream, inside the timed
@@ -150,6 +151,48 @@ def decode_case(lens, hkv, d, bs, partition, steps, warmup, seed=0, hq=None):
     return res
 
 
+def cache_write_case(tokens, hkv, d, bs, steps, warmup, seed=0):
+    """Paged KV-cache writer: ``tokens`` new K/V rows (a batch of prompts)
+    scattered into a shuffled page pool; bytes = K+V read + written."""
+    import numpy as np
+    import torch
+
+    import attnkernels as ak
+    import oracle
+
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    key = torch.randn(tokens, hkv, d, generator=g, device="cuda", dtype=torch.float16)
+    value = torch.randn(tokens, hkv, d, generator=g, device="cuda", dtype=torch.float16)
+    pool = -(-tokens // bs) * 11 // 10 + 1
+    kc = torch.zeros(pool, hkv, bs, d, device="cuda", dtype=torch.float16)
+    vc = torch.zeros_like(kc)
+    pages = np.random.default_rng(seed).permutation(pool)[: -(-tokens // bs)]
+    slots_np = (pages[np.arange(tokens) // bs] * bs + np.arange(tokens) % bs).astype(np.int64)
+    slots = torch.from_numpy(slots_np).cuda()
+    fn = lambda: ak.reshape_and_cache(key, value, kc, vc, slots)  # noqa: E731
+    fn()
+    torch.cuda.synchronize()
+    sub = slice(0, min(tokens, 2048))  # bit-exact check of a prefix of the tokens against the oracle
+    want_k, _ = oracle.reshape_and_cache(key[sub].cpu().numpy(), value[sub].cpu().numpy(),
+                                         np.zeros((pool, hkv, bs, d), np.float16), np.zeros((pool, hkv, bs, d), np.float16),
+                                         slots_np[sub])
+    got = kc.cpu().numpy()
+    touched = pages[: -(-sub.stop // bs)]
+    mism = int((got[touched] != want_k[touched]).sum())
+    total_ms, ev_mean, ev_med = timed_steps(fn, steps, warmup)
+    nbytes = 2 * tokens * hkv * d * 2 * 2 + tokens * 8
+    ms = total_ms / steps
+    res = dict(workload=f"paged cache write T={tokens} Hkv={hkv} D={d} bs={bs} fp16 (shuffled pages)",
+               value=round(nbytes / (ms * 1e-3) / 1e9, 1), unit="GB/s", ms_per_step=round(ms, 4),
+               kernel_ms_mean=round(ev_mean, 4), kernel_ms_median=round(ev_med, 4),
+               kernel_gbs=round(nbytes / (ev_mean * 1e-3) / 1e9, 1),
+               frac_of_peak=round(nbytes / (ev_mean * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+               bytes_per_step=nbytes, mismatched_elements=mism)
+    del key, value, kc, vc
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(seconds):
     """The numpy fp32 oracle on (batch, head) slices of the headline workload,
     on this host's cores, for about ``seconds`` of CPU work."""
@@ -220,10 +263,13 @@ def main():
         "decode_ragged64_d128": lambda: decode_case(lens4, 32, 128, 16, 512, K, W),
         "decode_long8_d128": lambda: decode_case([32768] * 8, 32, 128, 16, 256, K, W),
         "decode_long8_d64": lambda: decode_case([32768] * 8, 32, 64, 16, 256, K, W),
+        # the step before decode reads the cache: append a batch of prompts' K/V to it
+        "cache_write_t16k": lambda: cache_write_case(16384, 32, 128, 16, K, W),
     }
     groups = {"all": list(cases), "headline": ["prefill_d128_n8192_causal"],
               "prefill": [c for c in cases if c.startswith("prefill")],
-              "decode": ["prefill_d128_n8192_causal"] + [c for c in cases if c.startswith("decode")]}
+              "decode": ["prefill_d128_n8192_causal"] + [c for c in cases if c.startswith("decode")],
+              "cache": ["prefill_d128_n8192_causal", "cache_write_t16k"]}
     selected = groups.get(args.only, [c for c in args.only.split(",") if c in cases])
     if not selected:
         raise SystemExit(f"--only: choose from {sorted(groups)} or a comma list of {sorted(cases)}")

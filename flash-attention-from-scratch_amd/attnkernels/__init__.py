@@ -11,6 +11,7 @@ accumulation and an online softmax; none materialises the N x N scores.
 
 Decode (one query token per sequence) over a paged KV cache:
     paged_decode      split-K ("flash-decoding") kernel plus an LSE-merge reduce
+    reshape_and_cache writes new tokens' K/V into that cache (fp16 or bf16)
 
 The native code (``libattnkernels.so``, C-ABI in ``include/attnkernels.h``, and
 the torch glue module ``attnkernels_ext``) is built in-tree by
@@ -27,7 +28,7 @@ import os
 import torch
 
 __all__ = ["naive_attention", "flash_attention", "paged_decode", "decode_partition",
-           "load_extension"]
+           "reshape_and_cache", "load_extension"]
 
 CHUNK = 256  # partitions are multiples of it (reference attnkernels/__init__.py:29)
 
@@ -149,3 +150,40 @@ def paged_decode(q, k_cache, v_cache, block_tables, context_lens, max_context_le
         q.contiguous(), k_cache.contiguous(), v_cache.contiguous(),
         block_tables.to(torch.int32).contiguous(), context_lens.to(torch.int32).contiguous(),
         int(max_context_len), float(scale), partition_size)
+
+
+def reshape_and_cache(key, value, k_cache, v_cache, slot_mapping):
+    """Write new tokens' keys and values into the paged caches, in place.
+
+    The step before ``paged_decode`` reads them (after a prefill, or after each
+    decode step); not part of the reference, whose decode only reads the cache
+    in the layout of attnkernels/reference.py:21-44.
+
+    key, value:   [T, H_kv, D] fp16 or bf16 (heads contiguous; any token stride,
+                  e.g. a slice of a fused QKV projection output)
+    k_cache:      [num_blocks, H_kv, block_size, D], same dtype (v_cache the same)
+    slot_mapping: [T] int64 (or int32): token t goes to page slot // block_size,
+                  row slot % block_size.  Negative slots (padding) and slots
+                  past the pool are skipped.
+    """
+    if key.dim() != 3 or value.shape != key.shape:
+        raise ValueError("key and value must be [num_tokens, H_kv, D] of the same shape")
+    if key.dtype not in (torch.float16, torch.bfloat16) or not (
+            key.dtype == value.dtype == k_cache.dtype == v_cache.dtype):
+        raise ValueError("key, value and the caches must all be fp16 or all bf16")
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape or \
+            (k_cache.shape[1], k_cache.shape[3]) != (key.shape[1], key.shape[2]):
+        raise ValueError("caches must be [num_blocks, H_kv, block_size, D] matching key")
+    if key.shape[-1] % 8:
+        raise ValueError("head_dim must be a multiple of 8")
+    if slot_mapping.dim() != 1 or slot_mapping.shape[0] != key.shape[0]:
+        raise ValueError("slot_mapping must be [num_tokens]")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("caches must be contiguous (they are written in place)")
+
+    def rows(x):  # heads contiguous, token stride a multiple of 8 elements
+        ok = x.stride(2) == 1 and x.stride(1) == x.shape[2] and (x.shape[0] <= 1 or x.stride(0) % 8 == 0)
+        return x if ok and x.data_ptr() % 16 == 0 else x.contiguous()
+
+    slots = slot_mapping.to(device=key.device, dtype=torch.int64).contiguous()  # a host tensor is copied over
+    load_extension().reshape_and_cache(rows(key), rows(value), k_cache, v_cache, slots)

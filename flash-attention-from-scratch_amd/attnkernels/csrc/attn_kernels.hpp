@@ -38,7 +38,19 @@ struct DecodeArgs {
     void* stream;
 };
 
+struct CacheWriteArgs {
+    const void* key;        // [num_tokens, hkv, head_dim], token stride key_stride elements
+    const void* value;      // [num_tokens, hkv, head_dim], token stride value_stride elements
+    void* k_cache;          // [num_blocks, hkv, bs, head_dim]
+    void* v_cache;
+    const int64_t* slots;   // [num_tokens]
+    int64_t num_tokens, hkv, head_dim, num_blocks, bs;
+    int64_t key_stride, value_stride;  // multiples of 8
+    void* stream;
+};
+
 hipError_t prefill_launch(const PrefillArgs& a);
 hipError_t decode_launch(const DecodeArgs& a);
+hipError_t cache_write_launch(const CacheWriteArgs& a);
 
 }  // namespace ak

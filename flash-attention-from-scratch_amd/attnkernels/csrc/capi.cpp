@@ -164,4 +164,43 @@ int ak_paged_decode(const void* q, const void* k_cache, const void* v_cache, con
     return hip_status(ak::decode_launch(a), "paged_decode");
 }
 
+int ak_reshape_and_cache(const void* key, const void* value, void* k_cache, void* v_cache,
+                         const int64_t* slot_mapping, int64_t num_tokens, int64_t num_kv_heads,
+                         int64_t head_dim, int64_t num_blocks, int64_t block_size, int64_t key_stride,
+                         int64_t value_stride, void* stream) {
+    if (num_tokens < 0 || num_kv_heads <= 0 || num_blocks < 0 || block_size <= 0)
+        return fail(AK_ERR_INVALID_ARGUMENT, "reshape_and_cache: invalid size");
+    if (head_dim <= 0 || head_dim % 8 != 0 || head_dim > 512)
+        return fail(AK_ERR_UNSUPPORTED, "reshape_and_cache: head_dim must be a multiple of 8 up to 512");
+    const int64_t row = num_kv_heads * head_dim;
+    if (key_stride < row || value_stride < row || key_stride % 8 || value_stride % 8)
+        return fail(AK_ERR_INVALID_ARGUMENT,
+                    "reshape_and_cache: token strides must be multiples of 8 and >= num_kv_heads * head_dim");
+    if (num_tokens == 0 || num_blocks == 0) return ok();  // nothing to write, or no slot in range
+    if (!key || !value || !k_cache || !v_cache || !slot_mapping)
+        return fail(AK_ERR_INVALID_ARGUMENT, "reshape_and_cache: null pointer");
+    if (!aligned16(key) || !aligned16(value) || !aligned16(k_cache) || !aligned16(v_cache) ||
+        (reinterpret_cast<uintptr_t>(slot_mapping) & 7u))
+        return fail(AK_ERR_INVALID_ARGUMENT, "reshape_and_cache: tensors must be 16-byte aligned");
+    // Grid: x = token (< 2^31), y = groups of 256 chunks of one token (<= 65535).
+    if (num_kv_heads * (head_dim / 8) > 65535LL * 256 || block_size > INT_MAX ||
+        num_blocks > INT64_MAX / block_size / row || num_tokens > INT_MAX)
+        return fail(AK_ERR_INVALID_ARGUMENT, "reshape_and_cache: size out of range");
+    ak::CacheWriteArgs a{};
+    a.key = key;
+    a.value = value;
+    a.k_cache = k_cache;
+    a.v_cache = v_cache;
+    a.slots = slot_mapping;
+    a.num_tokens = num_tokens;
+    a.hkv = num_kv_heads;
+    a.head_dim = head_dim;
+    a.num_blocks = num_blocks;
+    a.bs = block_size;
+    a.key_stride = key_stride;
+    a.value_stride = value_stride;
+    a.stream = stream;
+    return hip_status(ak::cache_write_launch(a), "reshape_and_cache");
+}
+
 }  // extern "C"

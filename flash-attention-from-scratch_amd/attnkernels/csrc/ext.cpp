@@ -1,5 +1,6 @@
 // Thin PyTorch-ROCm glue: the pybind module `attnkernels_ext` with the
-// reference's four functions (attnkernels/csrc/ext.cpp:3-17), each allocating
+// reference's four functions (attnkernels/csrc/ext.cpp:3-17) plus the paged
+// cache writer reshape_and_cache, each allocating
 // its output (and split-K workspace) from the caching allocator and calling
 // the C-ABI in include/attnkernels.h on the caller's current HIP stream.
 #include <torch/extension.h>
@@ -86,10 +87,39 @@ torch::Tensor paged_decode(torch::Tensor q, torch::Tensor kc, torch::Tensor vc, 
     return out;
 }
 
+// In place: writes key/value rows into the caches (no counterpart in the
+// reference, whose decode only reads the cache).
+void reshape_and_cache(torch::Tensor key, torch::Tensor value, torch::Tensor kc, torch::Tensor vc,
+                       torch::Tensor slots) {
+    TORCH_CHECK(key.is_cuda() && key.dim() == 3 && value.dim() == 3 && key.sizes() == value.sizes(),
+                "key and value must be GPU tensors [num_tokens, H_kv, D] of the same shape");
+    TORCH_CHECK(key.element_size() == 2 && value.scalar_type() == key.scalar_type() &&
+                    kc.scalar_type() == key.scalar_type() && vc.scalar_type() == key.scalar_type(),
+                "key, value and the caches must share one 2-byte dtype (fp16 or bf16)");
+    TORCH_CHECK(key.stride(2) == 1 && key.stride(1) == key.size(2) && value.stride(2) == 1 &&
+                    value.stride(1) == value.size(2),
+                "key and value must have contiguous heads (any token stride)");
+    TORCH_CHECK(kc.dim() == 4 && kc.is_contiguous() && vc.is_contiguous() && vc.sizes() == kc.sizes() &&
+                    kc.size(1) == key.size(1) && kc.size(3) == key.size(2),
+                "k_cache and v_cache must be contiguous [num_blocks, H_kv, block_size, D] matching key");
+    TORCH_CHECK(slots.scalar_type() == torch::kLong && slots.dim() == 1 && slots.is_contiguous() &&
+                    slots.size(0) == key.size(0),
+                "slot_mapping must be a contiguous int64 tensor [num_tokens]");
+    for (const auto* t : {&value, &kc, &vc, &slots})
+        TORCH_CHECK(t->device() == key.device(), "all reshape_and_cache tensors must be on the same device");
+    const at::hip::HIPGuardMasqueradingAsCUDA guard(key.device());
+    const int64_t T = key.size(0);
+    check_rc(ak_reshape_and_cache(key.data_ptr(), value.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                  slots.data_ptr<int64_t>(), T, key.size(1), key.size(2), kc.size(0), kc.size(2),
+                                  T > 1 ? key.stride(0) : key.size(1) * key.size(2),
+                                  T > 1 ? value.stride(0) : value.size(1) * value.size(2), stream_of(key)));
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.doc() = "gfx950 attention kernels: MFMA flash prefill, paged split-K decode";
     m.def("naive_attention", &naive_attention, "prefill attention (served by the MFMA flash kernel)");
     m.def("flash_simt", &flash_simt, "prefill attention (served by the MFMA flash kernel)");
     m.def("flash_wmma", &flash_wmma, "tiled attention with online softmax on MFMA matrix cores");
     m.def("paged_decode", &paged_decode, "decode attention over a paged KV cache, split-K");
+    m.def("reshape_and_cache", &reshape_and_cache, "write new tokens' K/V rows into the paged caches");
 }

@@ -90,6 +90,25 @@ int ak_paged_decode(const void *q, const void *k_cache, const void *v_cache,
                     int64_t max_context_len, double scale, int64_t partition, void *workspace,
                     size_t workspace_bytes, void *stream);
 
+/* Paged KV-cache writer ("reshape and cache"): appends new tokens' keys and
+ * values to the paged cache that ak_paged_decode reads.  No counterpart in the
+ * reference, which only reads the cache (attnkernels/csrc/paged_decode.cu:95-96);
+ * the layout written is the reference's (attnkernels/reference.py:21-44).
+ *   key, value:   [num_tokens, num_kv_heads, head_dim], 2-byte elements (fp16 or
+ *                 bf16, copied bit for bit); token t starts key_stride (value_stride)
+ *                 elements after token t-1, heads are contiguous (a row of a
+ *                 larger projection output may be passed with its stride)
+ *   k_cache, v_cache: [num_blocks, num_kv_heads, block_size, head_dim], same dtype
+ *   slot_mapping: int64 [num_tokens]; token t is written to page
+ *                 slot / block_size, row slot % block_size.  Negative slots
+ *                 (padding) and slots >= num_blocks * block_size are skipped.
+ * head_dim a multiple of 8 up to 512; strides multiples of 8 and >= num_kv_heads *
+ * head_dim.  Two tokens with the same slot: one of them wins. */
+int ak_reshape_and_cache(const void *key, const void *value, void *k_cache, void *v_cache,
+                         const int64_t *slot_mapping, int64_t num_tokens, int64_t num_kv_heads,
+                         int64_t head_dim, int64_t num_blocks, int64_t block_size,
+                         int64_t key_stride, int64_t value_stride, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -12,6 +12,11 @@ function (closed forms, a float64 brute force written independently in C in
 ``attn_f64.c``, torch's CPU attention routine, the reference's recorded
 ``decode_partition`` values, planted-mistake checks) lives in
 ``tests/test_oracle.py``.  No function here is left "parity unpinned".
+
+``reshape_and_cache`` and ``append_slots`` restate the paged-cache writer,
+which has no counterpart in the reference: they follow the cache layout the
+reference reads (attnkernels/reference.py:21-51, paged_decode.cu:95-96) and are
+pinned by round trips through ``gather_kv`` and an element-wise loop.
 """
 from __future__ import annotations
 
@@ -215,3 +220,32 @@ def paged_decode_splitk(q, k_cache, v_cache, block_tables, context_lens, max_con
     if S == 1:
         return o[:, :, 0]
     return merge_partials(m, l, o, context_lens, partition)
+
+
+def append_slots(block_tables, positions, block_size):
+    """Cache slot of token ``positions[b]`` of sequence b: the page the block
+    table holds for it times block_size plus the row in the page (the address
+    map of paged_decode.cu:95-96 / reference.py:47-51, written as one index).
+    A negative position gives slot -1 (skip)."""
+    bt = np.asarray(block_tables)
+    pos = np.asarray(positions, dtype=np.int64)
+    slots = np.full(pos.shape, -1, dtype=np.int64)
+    ok = pos >= 0
+    rows = np.nonzero(ok)[0]
+    slots[ok] = bt[rows, pos[ok] // block_size].astype(np.int64) * block_size + pos[ok] % block_size
+    return slots
+
+
+def reshape_and_cache(key, value, k_cache, v_cache, slot_mapping):
+    """Write token t of key/value [T, Hkv, D] to page slot // bs, row slot % bs
+    of copies of the caches [num_blocks, Hkv, bs, D]; negative slots and slots
+    past the pool are skipped.  Bit copy: the dtype is kept.  Returns the new
+    (k_cache, v_cache)."""
+    kc, vc = np.array(k_cache, copy=True), np.array(v_cache, copy=True)
+    nb, _, bs, _ = kc.shape
+    slots = np.asarray(slot_mapping, dtype=np.int64)
+    ok = (slots >= 0) & (slots < nb * bs)
+    t = np.nonzero(ok)[0]
+    kc[slots[ok] // bs, :, slots[ok] % bs, :] = np.asarray(key)[t]
+    vc[slots[ok] // bs, :, slots[ok] % bs, :] = np.asarray(value)[t]
+    return kc, vc

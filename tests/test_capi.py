@@ -32,6 +32,7 @@ def lib():
     L.ak_paged_decode_workspace_size.argtypes = [i64] * 5
     L.ak_paged_decode_workspace_size.restype = ctypes.c_size_t
     L.ak_paged_decode.argtypes = [vp] * 6 + [i64] * 8 + [f64, i64, vp, ctypes.c_size_t, vp]
+    L.ak_reshape_and_cache.argtypes = [vp] * 5 + [i64] * 7 + [vp]
     return L
 
 
@@ -111,3 +112,23 @@ def test_paged_decode_rejects_bad_sizes(lib):
     assert decode(lib, bs=0) == 1
     assert decode(lib, maxb=0) == 1
     assert decode(lib, B=0) == 0  # nothing to do
+
+
+def test_reshape_and_cache_validation(lib):
+    # key, value, k_cache, v_cache, slots, T, Hkv, D, num_blocks, bs, key_stride, value_stride
+    rc = lib.ak_reshape_and_cache(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 8, 12, 10, 16, 96, 96, None)
+    assert rc == 2 and b"head_dim must be a multiple of 8" in lib.ak_last_error()
+    rc = lib.ak_reshape_and_cache(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 8, 128, 10, 16, 512, 1024, None)
+    assert rc == 1 and b"token strides" in lib.ak_last_error()
+    rc = lib.ak_reshape_and_cache(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 8, 128, 10, 16, 1028, 1024, None)
+    assert rc == 1 and b"token strides" in lib.ak_last_error()
+    rc = lib.ak_reshape_and_cache(FAKE, FAKE, FAKE, FAKE, FAKE, -1, 8, 128, 10, 16, 1024, 1024, None)
+    assert rc == 1 and b"invalid size" in lib.ak_last_error()
+    rc = lib.ak_reshape_and_cache(FAKE, None, FAKE, FAKE, FAKE, 4, 8, 128, 10, 16, 1024, 1024, None)
+    assert rc == 1 and b"null pointer" in lib.ak_last_error()
+    rc = lib.ak_reshape_and_cache(ctypes.c_void_p(4104), FAKE, FAKE, FAKE, FAKE, 4, 8, 128, 10, 16, 1024, 1024,
+                                  None)
+    assert rc == 1 and b"16-byte aligned" in lib.ak_last_error()
+    # nothing to write: no GPU work, no pointer use
+    assert lib.ak_reshape_and_cache(None, None, None, None, None, 0, 8, 128, 10, 16, 1024, 1024, None) == 0
+    assert lib.ak_reshape_and_cache(None, None, None, None, None, 4, 8, 128, 0, 16, 1024, 1024, None) == 0

@@ -262,3 +262,73 @@ def test_workload_conventions():
     assert oracle.prefill_flops(2, 32, 8192, 128, True) == pytest.approx(1.0995e12, rel=1e-4)
     assert oracle.prefill_flops(4, 16, 2048, 64, False) == pytest.approx(6.872e10, rel=1e-3)
     assert oracle.decode_kv_bytes([32768] * 8, 32, 128) == 4294967296
+
+
+# ------------------------------------------------------- paged cache writer --
+
+def _write_loop(key, value, kc, vc, slots):
+    """Element-by-element restatement: cache[slot // bs, h, slot % bs, d] = key[t, h, d]."""
+    kc, vc = kc.copy(), vc.copy()
+    nb, hkv, bs, d = kc.shape
+    for t, s in enumerate(slots):
+        if 0 <= s < nb * bs:
+            for h in range(hkv):
+                for j in range(d):
+                    kc[s // bs, h, s % bs, j] = key[t, h, j]
+                    vc[s // bs, h, s % bs, j] = value[t, h, j]
+    return kc, vc
+
+
+def test_append_slots_known_answers():
+    bt = np.array([[7, 3, 9], [2, 5, 0]], np.int32)
+    assert oracle.append_slots(bt, [0, 17], 16).tolist() == [7 * 16, 5 * 16 + 1]
+    assert oracle.append_slots(bt, [47, -1], 16).tolist() == [9 * 16 + 15, -1]
+
+
+@pytest.mark.parametrize("dtype", [np.float16, np.uint16])  # uint16 stands in for raw bf16 bits
+def test_reshape_and_cache_equals_elementwise_loop(dtype):
+    r = np.random.default_rng(3)
+    kc = r.integers(0, 60000, (6, 2, 4, 8)).astype(np.uint16).view(dtype)
+    vc = r.integers(0, 60000, (6, 2, 4, 8)).astype(np.uint16).view(dtype)
+    key = r.integers(0, 60000, (5, 2, 8)).astype(np.uint16).view(dtype)
+    value = r.integers(0, 60000, (5, 2, 8)).astype(np.uint16).view(dtype)
+    slots = np.array([3, -1, 23, 24, 9], np.int64)  # 24 = past the pool of 6 * 4 slots
+    got_k, got_v = oracle.reshape_and_cache(key, value, kc, vc, slots)
+    want_k, want_v = _write_loop(key, value, kc, vc, slots)
+    assert got_k.view(np.uint16).tolist() == want_k.view(np.uint16).tolist()
+    assert got_v.view(np.uint16).tolist() == want_v.view(np.uint16).tolist()
+    assert got_k.dtype == dtype
+
+
+def test_reshape_and_cache_round_trip_through_gather():
+    """Appending every token of every sequence through its block table, then
+    gathering the pages, gives the tokens back in order (reference.py:47-51)."""
+    lens = [37, 5, 16]
+    kc0, vc0, bt, _ = oracle.make_paged_cache(lens, 3, 16, block_size=8, seed=4)
+    r = np.random.default_rng(5)
+    toks = [r.standard_normal((c, 3, 16)).astype(np.float16) for c in lens]
+    kc, vc = np.zeros_like(kc0), np.zeros_like(vc0)
+    for b, c in enumerate(lens):
+        slots = oracle.append_slots(np.repeat(bt[b:b + 1], c, 0), np.arange(c), 8)
+        kc, vc = oracle.reshape_and_cache(toks[b], -toks[b], kc, vc, slots)
+    nb = bt.shape[1]
+    for b, c in enumerate(lens):
+        got = oracle.gather_kv(kc, bt[b:b + 1], nb)[0][:, :c]       # [Hkv, c, D]
+        assert np.array_equal(got, toks[b].transpose(1, 0, 2))
+        assert np.array_equal(oracle.gather_kv(vc, bt[b:b + 1], nb)[0][:, :c], -toks[b].transpose(1, 0, 2))
+
+
+def test_planted_writer_mistake_is_caught():
+    """Page and row swapped (slot % bs as the page): the round trip fails."""
+    lens = [20]
+    kc0, _, bt, _ = oracle.make_paged_cache(lens, 2, 8, block_size=4, seed=6)
+    toks = np.random.default_rng(7).standard_normal((20, 2, 8)).astype(np.float16)
+    slots = oracle.append_slots(np.repeat(bt, 20, 0), np.arange(20), 4)
+    bad = np.zeros_like(kc0)
+    nb_pool = bad.shape[0]
+    for t, s in enumerate(slots):
+        page, row = s % 4, (s // 4) % 4
+        if page < nb_pool:
+            bad[page, :, row, :] = toks[t]
+    got = oracle.gather_kv(bad, bt, bt.shape[1])[0][:, :20]
+    assert not np.array_equal(got, toks.transpose(1, 0, 2))
