@@ -11,7 +11,7 @@ The same line carries, under ``workloads``, the other BASELINE configs measured
 the same way: non-causal prefill, the N=8191 variant, the two
 paged split-K decode configs in KV GB/s with the reference's byte convention
 sum(ctx)*Hkv*D*2*2 (bench/bench.py:199-200), and the paged cache writer
-(K/V rows read + written, GB/s).
+(K/V rows read + written, GB/s), and a packed variable-length GQA prefill.
 
 ``roofline`` is the headline kernel's algorithmic FLOP per launch divided by its
 mean launch duration (HIP events on the launch stream, inside the timed
@@ -151,6 +151,44 @@ def decode_case(lens, hkv, d, bs, partition, steps, warmup, seed=0, hq=None):
     return res
 
 
+def varlen_case(lens, h, hkv, d, causal, steps, warmup, seed=0):
+    """Packed variable-length causal prefill with GQA (no padding): FLOP is the
+    sum over sequences of the reference convention 4*H*n^2*D(/2 if causal)."""
+    import numpy as np
+    import torch
+
+    import attnkernels as ak
+    import oracle
+
+    total = sum(lens)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    q = torch.randn(total, h, d, generator=g, device="cuda", dtype=torch.float16)
+    k = torch.randn(total, hkv, d, generator=g, device="cuda", dtype=torch.float16)
+    v = torch.randn(total, hkv, d, generator=g, device="cuda", dtype=torch.float16)
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32, device="cuda")
+    fn = lambda: ak.flash_attention_varlen(q, k, v, cu, max(lens), causal=causal)  # noqa: E731
+    out = fn()
+    torch.cuda.synchronize()
+    n0 = lens[0]  # first sequence, first 2 heads (one kv head) through the oracle
+    ref = oracle.attention_gqa(q[:n0, :2].cpu().numpy().transpose(1, 0, 2), k[:n0, :1].cpu().numpy().transpose(1, 0, 2),
+                               v[:n0, :1].cpu().numpy().transpose(1, 0, 2), causal)
+    err = float(np.abs(out[:n0, :2].float().cpu().numpy() - ref.transpose(1, 0, 2)).max())
+    del out
+    total_ms, ev_mean, ev_med = timed_steps(fn, steps, warmup)
+    flops = sum(oracle.prefill_flops(1, h, n, d, causal) for n in lens)
+    ms = total_ms / steps
+    res = dict(workload=f"varlen prefill {len(lens)} seqs total={total} max={max(lens)} H={h} Hkv={hkv} D={d} "
+                        f"{'causal' if causal else 'non-causal'}",
+               value=round(flops / (ms * 1e-3) / 1e12, 2), unit="TFLOP/s", ms_per_step=round(ms, 4),
+               kernel_ms_mean=round(ev_mean, 4), kernel_ms_median=round(ev_med, 4),
+               kernel_tflops=round(flops / (ev_mean * 1e-3) / 1e12, 2),
+               frac_of_peak=round(flops / (ev_mean * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
+               flop_per_launch=flops, max_abs_err=float(f"{err:.3g}"))
+    del q, k, v
+    torch.cuda.empty_cache()
+    return res
+
+
 def cache_write_case(tokens, hkv, d, bs, steps, warmup, seed=0):
     """Paged KV-cache writer: ``tokens`` new K/V rows (a batch of prompts)
     scattered into a shuffled page pool; bytes = K+V read + written."""
@@ -256,6 +294,7 @@ def main():
         torch.cuda.empty_cache()
     K, W = args.steps, args.warmup
     lens4 = torch.randint(1, 4097, (64,), generator=torch.Generator().manual_seed(4)).tolist()
+    lensv = torch.randint(512, 8193, (16,), generator=torch.Generator().manual_seed(5)).tolist()
     cases = {  # BASELINE.json configs[1..4]
         "prefill_d128_n8192_causal": lambda: prefill_case(2, 32, 8192, 128, True, K, W),
         "prefill_d64_n2048": lambda: prefill_case(4, 16, 2048, 64, False, K, W),
@@ -263,11 +302,14 @@ def main():
         "decode_ragged64_d128": lambda: decode_case(lens4, 32, 128, 16, 512, K, W),
         "decode_long8_d128": lambda: decode_case([32768] * 8, 32, 128, 16, 256, K, W),
         "decode_long8_d64": lambda: decode_case([32768] * 8, 32, 64, 16, 256, K, W),
+        # packed prompts of mixed lengths, 4 query heads per kv head, no padding
+        "prefill_varlen_gqa": lambda: varlen_case(lensv, 32, 8, 128, True, K, W),
         # the step before decode reads the cache: append a batch of prompts' K/V to it
         "cache_write_t16k": lambda: cache_write_case(16384, 32, 128, 16, K, W),
     }
     groups = {"all": list(cases), "headline": ["prefill_d128_n8192_causal"],
               "prefill": [c for c in cases if c.startswith("prefill")],
+              "layouts": ["prefill_d128_n8192_causal", "prefill_varlen_gqa", "cache_write_t16k"],
               "decode": ["prefill_d128_n8192_causal"] + [c for c in cases if c.startswith("decode")],
               "cache": ["prefill_d128_n8192_causal", "cache_write_t16k"]}
     selected = groups.get(args.only, [c for c in args.only.split(",") if c in cases])

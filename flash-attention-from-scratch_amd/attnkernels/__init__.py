@@ -7,7 +7,10 @@ Prefill (many query tokens per sequence):
     naive_attention   softmax(scale Q K^T [+ causal mask]) V
     flash_attention   same maths; variant "simt" or "wmma" as in the reference
 All three run one gfx950 flash kernel on the f16 MFMA matrix cores with fp32
-accumulation and an online softmax; none materialises the N x N scores.
+accumulation and an online softmax; none materialises the N x N scores.  The
+same kernel also serves two layouts the reference does not have:
+    flash_attention_gqa     fewer kv heads than query heads (GQA / MQA)
+    flash_attention_varlen  packed variable-length sequences, no padding
 
 Decode (one query token per sequence) over a paged KV cache:
     paged_decode      split-K ("flash-decoding") kernel plus an LSE-merge reduce
@@ -28,7 +31,7 @@ import os
 import torch
 
 __all__ = ["naive_attention", "flash_attention", "paged_decode", "decode_partition",
-           "reshape_and_cache", "load_extension"]
+           "reshape_and_cache", "flash_attention_gqa", "flash_attention_varlen", "load_extension"]
 
 CHUNK = 256  # partitions are multiples of it (reference attnkernels/__init__.py:29)
 
@@ -150,6 +153,58 @@ def paged_decode(q, k_cache, v_cache, block_tables, context_lens, max_context_le
         q.contiguous(), k_cache.contiguous(), v_cache.contiguous(),
         block_tables.to(torch.int32).contiguous(), context_lens.to(torch.int32).contiguous(),
         int(max_context_len), float(scale), partition_size)
+
+
+def flash_attention_gqa(q, k, v, causal=False, scale=None):
+    """Prefill with grouped-query attention: q [B, H, N, D], k and v [B, H_kv,
+    N, D] fp16 with H a multiple of H_kv; query head h reads kv head
+    h // (H / H_kv).  Same kernel as ``flash_attention``, which (like the
+    reference, attnkernels/__init__.py:57-58) requires H_kv == H."""
+    for t in (q, k, v):
+        if not (t.is_cuda and t.dtype == torch.float16 and t.dim() == 4):
+            raise ValueError("q, k, v must be fp16 CUDA tensors of shape [B, H, N, D]")
+    if k.shape != v.shape or (k.shape[0], k.shape[2], k.shape[3]) != (q.shape[0], q.shape[2], q.shape[3]):
+        raise ValueError("k and v must be [B, H_kv, N, D] with the B, N and D of q")
+    if k.shape[1] == 0 or q.shape[1] % k.shape[1]:
+        raise ValueError("the query heads must be a multiple of the kv heads")
+    if q.shape[-1] not in (64, 128):
+        raise ValueError("head_dim must be 64 or 128")
+    scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
+    return load_extension().flash_gqa(q.contiguous(), k.contiguous(), v.contiguous(), causal, float(scale))
+
+
+def flash_attention_varlen(q, k, v, cu_seqlens, max_seqlen, causal=False, scale=None):
+    """Prefill over packed variable-length sequences (no padding).
+
+    q: [total, H, D], k and v: [total, H_kv, D] fp16 (H a multiple of H_kv);
+    sequence b is rows cu_seqlens[b] .. cu_seqlens[b+1]-1 and attends only to
+    itself (causal: key j <= query i within the sequence).  cu_seqlens: int32
+    [B + 1]; max_seqlen: Python int >= every length (it sizes the grid).  A
+    host cu_seqlens is checked here; a device one is used as given (no sync):
+    inconsistent offsets then give wrong rows, never an out-of-bounds access.
+    """
+    for t in (q, k, v):
+        if not (t.is_cuda and t.dtype == torch.float16 and t.dim() == 3):
+            raise ValueError("q, k, v must be fp16 CUDA tensors of shape [total, H, D]")
+    if k.shape != v.shape or (k.shape[0], k.shape[2]) != (q.shape[0], q.shape[2]):
+        raise ValueError("k and v must be [total, H_kv, D] with the total and D of q")
+    if k.shape[1] == 0 or q.shape[1] % k.shape[1]:
+        raise ValueError("the query heads must be a multiple of the kv heads")
+    if q.shape[-1] not in (64, 128):
+        raise ValueError("head_dim must be 64 or 128")
+    if cu_seqlens.dim() != 1 or cu_seqlens.shape[0] < 1:
+        raise ValueError("cu_seqlens must be [B + 1]")
+    if not cu_seqlens.is_cuda:
+        c = cu_seqlens.to(torch.int64)
+        lens = c[1:] - c[:-1]
+        if (lens < 0).any() or (c.numel() and (c[0] < 0 or c[-1] > q.shape[0])):
+            raise ValueError("cu_seqlens must be non-decreasing offsets into the packed rows")
+        if lens.numel() and int(lens.max()) > int(max_seqlen):
+            raise ValueError("max_seqlen is shorter than a sequence")
+    scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
+    cu = cu_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
+    return load_extension().flash_varlen(q.contiguous(), k.contiguous(), v.contiguous(), cu, int(max_seqlen),
+                                         causal, float(scale))
 
 
 def reshape_and_cache(key, value, k_cache, v_cache, slot_mapping):

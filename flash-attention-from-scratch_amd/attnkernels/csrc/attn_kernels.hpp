@@ -13,8 +13,12 @@ struct PrefillArgs {
     const void* k;
     const void* v;
     void* o;
-    int64_t bh;      // batch * heads
-    int64_t n;       // sequence length
+    int64_t bh;      // batch * query heads
+    int64_t n;       // sequence length (packed layout: the longest sequence)
+    int64_t hq;      // query heads
+    int64_t hkv;     // kv heads, dividing hq
+    const int32_t* cu;  // packed layout: [batch + 1] sequence starts; nullptr: dense [B, H, N, D]
+    int64_t total_rows; // packed layout: rows of q/k/v; every sequence is clamped into [0, total_rows)
     int d;           // head dim, 64 or 128
     bool causal;
     float sl2;       // |scale| * log2(e)

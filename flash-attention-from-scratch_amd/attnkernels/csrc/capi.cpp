@@ -32,15 +32,23 @@ int hip_status(hipError_t e, const char* who) {
     return fail(AK_ERR_HIP, std::string(who) + ": HIP error: " + hipGetErrorString(e));
 }
 
+// Shared by every prefill entry point.  kv_heads divides heads (GQA); cu is
+// null for the dense [B, H, N, D] layout, else the packed layout's sequence
+// starts with total_rows rows in q/k/v and seq_len the longest sequence.
 int prefill(const char* who, const void* q, const void* k, const void* v, void* o, int64_t batch,
-            int64_t heads, int64_t seq_len, int64_t head_dim, int causal, double scale, void* stream) {
-    if (batch < 0 || heads < 0 || seq_len < 0)
+            int64_t heads, int64_t kv_heads, int64_t seq_len, int64_t head_dim, int causal, double scale,
+            const int32_t* cu, int64_t total_rows, void* stream) {
+    if (batch < 0 || heads < 0 || seq_len < 0 || kv_heads < 0 || total_rows < 0)
         return fail(AK_ERR_INVALID_ARGUMENT, std::string(who) + ": negative size");
-    if (batch * heads * seq_len == 0) return ok();  // empty output, nothing to launch
+    if (kv_heads == 0 ? heads != 0 : heads % kv_heads != 0)
+        return fail(AK_ERR_INVALID_ARGUMENT, std::string(who) + ": num_heads must be a multiple of num_kv_heads");
+    if (batch * heads * seq_len == 0 || (cu && total_rows == 0)) return ok();  // nothing to compute
     if (!q || !k || !v || !o) return fail(AK_ERR_INVALID_ARGUMENT, std::string(who) + ": null pointer");
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
         return fail(AK_ERR_INVALID_ARGUMENT, std::string(who) + ": pointers must be 16-byte aligned");
-    if (seq_len > INT_MAX / 2 || batch * heads > INT_MAX)
+    // Workgroups = query-tile units (256 rows, causal: pairs) x batch x heads: an int.
+    const int64_t tiles = (seq_len + 255) / 256, units = causal ? (tiles + 1) / 2 : tiles;
+    if (seq_len > INT_MAX / 2 || total_rows > INT_MAX / 2 || batch * heads > INT_MAX / units)
         return fail(AK_ERR_INVALID_ARGUMENT, std::string(who) + ": size out of range");
     ak::PrefillArgs a{};
     a.q = q;
@@ -48,6 +56,10 @@ int prefill(const char* who, const void* q, const void* k, const void* v, void* 
     a.v = v;
     a.o = o;
     a.bh = batch * heads;
+    a.hq = heads;
+    a.hkv = kv_heads;
+    a.cu = cu;
+    a.total_rows = total_rows;
     a.n = seq_len;
     a.d = (int)head_dim;
     a.causal = causal != 0;
@@ -72,14 +84,16 @@ int ak_naive_attention(const void* q, const void* k, const void* v, void* o, int
                        void* stream) {
     if (head_dim != 64 && head_dim != 128)
         return fail(AK_ERR_UNSUPPORTED, "naive_attention: head_dim must be 64 or 128");
-    return prefill("naive_attention", q, k, v, o, batch, heads, seq_len, head_dim, causal, scale, stream);
+    return prefill("naive_attention", q, k, v, o, batch, heads, heads, seq_len, head_dim, causal, scale, nullptr, 0,
+                   stream);
 }
 
 int ak_flash_simt(const void* q, const void* k, const void* v, void* o, int64_t batch, int64_t heads,
                   int64_t seq_len, int64_t head_dim, int causal, double scale, void* stream) {
     if (head_dim != 64 && head_dim != 128)
         return fail(AK_ERR_UNSUPPORTED, "flash_simt: head_dim must be 64 or 128");
-    return prefill("flash_simt", q, k, v, o, batch, heads, seq_len, head_dim, causal, scale, stream);
+    return prefill("flash_simt", q, k, v, o, batch, heads, heads, seq_len, head_dim, causal, scale, nullptr, 0,
+                   stream);
 }
 
 int ak_flash_wmma(const void* q, const void* k, const void* v, void* o, int64_t batch, int64_t heads,
@@ -87,7 +101,28 @@ int ak_flash_wmma(const void* q, const void* k, const void* v, void* o, int64_t 
                   void* stream) {
     if ((head_dim != 64 && head_dim != 128) || (block_n != 32 && block_n != 64))
         return fail(AK_ERR_UNSUPPORTED, "flash_wmma: head_dim must be 64 or 128 and block_n 32 or 64");
-    return prefill("flash_wmma", q, k, v, o, batch, heads, seq_len, head_dim, causal, scale, stream);
+    return prefill("flash_wmma", q, k, v, o, batch, heads, heads, seq_len, head_dim, causal, scale, nullptr, 0,
+                   stream);
+}
+
+int ak_prefill_gqa(const void* q, const void* k, const void* v, void* o, int64_t batch, int64_t num_heads,
+                   int64_t num_kv_heads, int64_t seq_len, int64_t head_dim, int causal, double scale,
+                   void* stream) {
+    if (head_dim != 64 && head_dim != 128)
+        return fail(AK_ERR_UNSUPPORTED, "prefill_gqa: head_dim must be 64 or 128");
+    return prefill("prefill_gqa", q, k, v, o, batch, num_heads, num_kv_heads, seq_len, head_dim, causal, scale,
+                   nullptr, 0, stream);
+}
+
+int ak_prefill_varlen(const void* q, const void* k, const void* v, void* o, const int32_t* cu_seqlens,
+                      int64_t batch, int64_t total_rows, int64_t num_heads, int64_t num_kv_heads,
+                      int64_t max_seqlen, int64_t head_dim, int causal, double scale, void* stream) {
+    if (head_dim != 64 && head_dim != 128)
+        return fail(AK_ERR_UNSUPPORTED, "prefill_varlen: head_dim must be 64 or 128");
+    if (batch > 0 && (!cu_seqlens || (reinterpret_cast<uintptr_t>(cu_seqlens) & 3u)))
+        return fail(AK_ERR_INVALID_ARGUMENT, "prefill_varlen: cu_seqlens must be a 4-byte aligned int32 array");
+    return prefill("prefill_varlen", q, k, v, o, batch, num_heads, num_kv_heads, max_seqlen, head_dim, causal,
+                   scale, batch > 0 ? cu_seqlens : nullptr, total_rows, stream);
 }
 
 size_t ak_paged_decode_workspace_size(int64_t batch, int64_t num_heads, int64_t head_dim,

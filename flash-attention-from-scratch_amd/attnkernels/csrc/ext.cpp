@@ -1,6 +1,6 @@
 // Thin PyTorch-ROCm glue: the pybind module `attnkernels_ext` with the
 // reference's four functions (attnkernels/csrc/ext.cpp:3-17) plus the paged
-// cache writer reshape_and_cache, each allocating
+// cache writer reshape_and_cache and the GQA / varlen prefill, each allocating
 // its output (and split-K workspace) from the caching allocator and calling
 // the C-ABI in include/attnkernels.h on the caller's current HIP stream.
 #include <torch/extension.h>
@@ -57,6 +57,43 @@ torch::Tensor flash_wmma(torch::Tensor q, torch::Tensor k, torch::Tensor v, bool
     auto o = torch::empty_like(q);
     check_rc(ak_flash_wmma(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), q.size(0), q.size(1),
                            q.size(2), q.size(3), causal, scale, block_n, stream_of(q)));
+    return o;
+}
+
+// Dense prefill with fewer kv heads than query heads (GQA/MQA).
+torch::Tensor flash_gqa(torch::Tensor q, torch::Tensor k, torch::Tensor v, bool causal, double scale) {
+    for (const auto* t : {&q, &k, &v}) {
+        TORCH_CHECK(t->is_cuda() && t->scalar_type() == torch::kHalf && t->dim() == 4 && t->is_contiguous(),
+                    "q, k, v must be contiguous fp16 GPU tensors of shape [B, H, N, D]");
+        TORCH_CHECK(t->device() == q.device(), "q, k, v must be on the same device");
+    }
+    TORCH_CHECK(k.sizes() == v.sizes() && k.size(0) == q.size(0) && k.size(2) == q.size(2) && k.size(3) == q.size(3),
+                "k and v must be [B, H_kv, N, D] with q's B, N and D");
+    const at::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+    auto o = torch::empty_like(q);
+    check_rc(ak_prefill_gqa(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), q.size(0), q.size(1), k.size(1),
+                            q.size(2), q.size(3), causal, scale, stream_of(q)));
+    return o;
+}
+
+// Packed variable-length prefill: q [T, H, D], k/v [T, H_kv, D], cu_seqlens int32 [B + 1].
+torch::Tensor flash_varlen(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor cu, int64_t max_seqlen,
+                           bool causal, double scale) {
+    for (const auto* t : {&q, &k, &v}) {
+        TORCH_CHECK(t->is_cuda() && t->scalar_type() == torch::kHalf && t->dim() == 3 && t->is_contiguous(),
+                    "q, k, v must be contiguous fp16 GPU tensors of shape [total, H, D]");
+        TORCH_CHECK(t->device() == q.device(), "q, k, v must be on the same device");
+    }
+    TORCH_CHECK(k.sizes() == v.sizes() && k.size(0) == q.size(0) && k.size(2) == q.size(2),
+                "k and v must be [total, H_kv, D] with q's total and D");
+    TORCH_CHECK(cu.scalar_type() == torch::kInt && cu.dim() == 1 && cu.is_contiguous() && cu.size(0) >= 1 &&
+                    cu.device() == q.device(),
+                "cu_seqlens must be a contiguous int32 tensor [B + 1] on q's device");
+    const at::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+    auto o = torch::empty_like(q);
+    check_rc(ak_prefill_varlen(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), cu.data_ptr<int32_t>(),
+                               cu.size(0) - 1, q.size(0), q.size(1), k.size(1), max_seqlen, q.size(2), causal, scale,
+                               stream_of(q)));
     return o;
 }
 
@@ -122,4 +159,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("flash_wmma", &flash_wmma, "tiled attention with online softmax on MFMA matrix cores");
     m.def("paged_decode", &paged_decode, "decode attention over a paged KV cache, split-K");
     m.def("reshape_and_cache", &reshape_and_cache, "write new tokens' K/V rows into the paged caches");
+    m.def("flash_gqa", &flash_gqa, "dense prefill with grouped-query attention");
+    m.def("flash_varlen", &flash_varlen, "prefill over packed variable-length sequences");
 }

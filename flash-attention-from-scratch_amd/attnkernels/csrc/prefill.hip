@@ -92,17 +92,18 @@ __device__ __forceinline__ int v_chunk(int r, int c) {
 
 // Global -> LDS for one K (or V) tile, keys [k0, k0 + BN), asynchronous
 // (vmcnt).  Each wave writes LPW contiguous KB of the tile; lane l fills the
-// 16-byte slot l of a KB.  Rows past n are clamped to row n-1: in bounds, and
-// masked to -inf later.
+// 16-byte slot l of a KB.  Row r starts r * rs elements after src.  Rows past n
+// are clamped to row n-1: in bounds, and masked to -inf later.
 template <int D, bool IS_V>
-__device__ __forceinline__ void load_kv(const f16* __restrict__ src, f16* dst, int k0, int n, int w, int lane) {
+__device__ __forceinline__ void load_kv(const f16* __restrict__ src, f16* dst, int k0, int n, int rs, int w,
+                                        int lane) {
     using T = PrefillTile<D>;
 #pragma unroll
     for (int j = 0; j < T::LPW; ++j) {
         const int blk = w * T::LPW + j;
         const int row = blk * T::RPI + lane / T::CPR, p = lane % T::CPR;
         const int c = IS_V ? v_chunk<D>(row, p) : k_chunk<D>(row, p);
-        __builtin_amdgcn_global_load_lds((AK_GLOBAL const void*)(src + (size_t)min(k0 + row, n - 1) * D + c * 8),
+        __builtin_amdgcn_global_load_lds((AK_GLOBAL const void*)(src + (size_t)min(k0 + row, n - 1) * rs + c * 8),
                                          (AK_LDS void*)(dst + blk * 512), 16, 0, 0);
     }
 }
@@ -252,7 +253,7 @@ constexpr int kValuPerMfma = 3, kExpPerMfma = 2, kKPrefetch = 2, kVPrefetch = 4;
 template <int D, bool CAUSAL>
 __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const f16* __restrict__ kb,
                                               const f16* __restrict__ vb, f16* __restrict__ ob,
-                                              f16* __restrict__ lds, int q0, int n, float sl2,
+                                              f16* __restrict__ lds, int q0, int n, int qs, int ks, float sl2,
                                               uint32_t qflip) {
     using T = PrefillTile<D>;
     const int tid = threadIdx.x;
@@ -269,16 +270,16 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
     // their keys are < n and (causal) <= the workgroup's first query row.
     const int kt_mask = min(nkt, CAUSAL ? q0 / T::BN : n / T::BN);
 
-    load_kv<D, false>(kb, kbuf, 0, n, w, lane);
-    load_kv<D, true>(vb, vbuf, 0, n, w, lane);
-    if (nkt > 1) load_kv<D, false>(kb, kbuf + T::TILE, T::BN, n, w, lane);
+    load_kv<D, false>(kb, kbuf, 0, n, ks, w, lane);
+    load_kv<D, true>(vb, vbuf, 0, n, ks, w, lane);
+    if (nkt > 1) load_kv<D, false>(kb, kbuf + T::TILE, T::BN, n, ks, w, lane);
 
     // Q as the MFMA B operand: col = query, k = head dim 16*dc + 8*half .. +7.
     f16x8 qf[T::DC];
 #pragma unroll
     for (int dc = 0; dc < T::DC; ++dc) {
         // Rows past n are clamped to n-1: computed, never stored.
-        f16x8 x = *reinterpret_cast<const f16x8*>(qb + (size_t)min(qrow, n - 1) * D + dc * 16 + half * 8);
+        f16x8 x = *reinterpret_cast<const f16x8*>(qb + (size_t)min(qrow, n - 1) * qs + dc * 16 + half * 8);
         if (qflip) {  // negative scale: fold the sign into Q exactly
             typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
             x = __builtin_bit_cast(f16x8, __builtin_bit_cast(u32x4, x) ^ qflip);
@@ -301,8 +302,8 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
     auto body = [&](int t, f32x16 (&sc)[T::KB], f32x16 (&sn)[T::KB], auto mask_tag) {
         constexpr bool MASK = decltype(mask_tag)::value;
         wait_loads_and_sync();  // K(t+1), V(t) landed; nobody reads K(t), V(t-1) any more
-        if (t + 2 < nkt) load_kv<D, false>(kb, kbuf + (t & 1) * T::TILE, (t + 2) * T::BN, n, w, lane);
-        if (t + 1 < nkt) load_kv<D, true>(vb, vbuf + ((t + 1) & 1) * T::TILE, (t + 1) * T::BN, n, w, lane);
+        if (t + 2 < nkt) load_kv<D, false>(kb, kbuf + (t & 1) * T::TILE, (t + 2) * T::BN, n, ks, w, lane);
+        if (t + 1 < nkt) load_kv<D, true>(vb, vbuf + ((t + 1) & 1) * T::TILE, (t + 1) * T::BN, n, ks, w, lane);
         // Causal: a tile whose first key is after this wave's last row is skipped.
         const bool act = !MASK || !CAUSAL || t * T::BN <= qw0 + T::QW - 1;
         if (act) {
@@ -351,7 +352,7 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
     const float l_tot = pair_sum(l_run);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     if (qrow < n) {
-        f16* orow = ob + (size_t)qrow * D + half * 8;
+        f16* orow = ob + (size_t)qrow * qs + half * 8;
 #pragma unroll
         for (int t2 = 0; t2 < T::DT; ++t2)
 #pragma unroll
@@ -364,40 +365,81 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
     }
 }
 
-template <int D, bool CAUSAL>
+// One workgroup per (sequence, query head, query-tile unit).  Query head h
+// reads kv head h / group.  Dense layout: q/o [B, Hq, N, D], k/v [B, Hkv, N, D].
+// Packed layout (VARLEN): q/o [total, Hq, D], k/v [total, Hkv, D], sequence b
+// being rows cu[b] .. cu[b+1]-1; the grid is sized for the longest sequence and
+// the units past a shorter one exit before touching memory.
+template <int D, bool CAUSAL, bool VARLEN>
 __global__ void __launch_bounds__(PrefillTile<D>::THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 flash_prefill_kernel(const f16* __restrict__ Q, const f16* __restrict__ K, const f16* __restrict__ V,
-                     f16* __restrict__ O, int n, int units_per_bh, int total_units, float sl2,
-                     uint32_t qflip) {
+                     f16* __restrict__ O, const int32_t* __restrict__ cu, int total_rows, int n_max,
+                     int units_per_bh, int total_units, int hq, int group, float sl2, uint32_t qflip) {
     using T = PrefillTile<D>;
     __shared__ __attribute__((aligned(1024))) f16 lds[2 * T::STAGE];
     const int L = xcd_remap((int)blockIdx.x, total_units);
-    const int bh = L / units_per_bh, u = L % units_per_bh;
-    const size_t base = (size_t)bh * n * D;
+    int bh, u;
+    if (VARLEN) {
+        // Highest units first: only the longest sequences have them, so the
+        // heaviest work starts early and short sequences fill the tail.
+        const int nbh = total_units / units_per_bh;
+        u = units_per_bh - 1 - L / nbh;
+        bh = L - (L / nbh) * nbh;
+    } else {
+        bh = L / units_per_bh;
+        u = L % units_per_bh;
+    }
+    const int b = bh / hq, h = bh - b * hq, hkv = hq / group, kvh = h / group;
+    int n, qs, ks;
+    size_t qbase, kvbase;
+    if (VARLEN) {
+        // Clamped into the tensors whatever the offsets hold: a bad cu gives a
+        // wrong answer, never an access out of bounds.
+        const int s0 = min(max(cu[b], 0), total_rows);
+        n = min(max(cu[b + 1], s0), total_rows) - s0;
+        qs = hq * D;
+        ks = hkv * D;
+        qbase = (size_t)s0 * qs + (size_t)h * D;
+        kvbase = (size_t)s0 * ks + (size_t)kvh * D;
+    } else {
+        n = n_max;
+        qs = ks = D;
+        qbase = (size_t)bh * n * D;
+        kvbase = ((size_t)b * hkv + kvh) * n * D;
+    }
     const int nqt = (n + T::BM - 1) / T::BM;
+    if (VARLEN && u >= (CAUSAL ? (nqt + 1) / 2 : nqt)) return;  // whole workgroup: past this sequence
+    const f16 *Qb = Q + qbase, *Kb = K + kvbase, *Vb = V + kvbase;
+    f16* Ob = O + qbase;
     if (CAUSAL) {
         // Pair the heaviest remaining tile with the lightest: equal work per workgroup.
         const int heavy = nqt - 1 - u;
-        prefill_qtile<D, true>(Q + base, K + base, V + base, O + base, lds, heavy * T::BM, n, sl2, qflip);
+        prefill_qtile<D, true>(Qb, Kb, Vb, Ob, lds, heavy * T::BM, n, qs, ks, sl2, qflip);
         if (u != heavy) {
             __syncthreads();  // every wave is done with the buffers before they are refilled
-            prefill_qtile<D, true>(Q + base, K + base, V + base, O + base, lds, u * T::BM, n, sl2, qflip);
+            prefill_qtile<D, true>(Qb, Kb, Vb, Ob, lds, u * T::BM, n, qs, ks, sl2, qflip);
         }
     } else {
-        prefill_qtile<D, false>(Q + base, K + base, V + base, O + base, lds, u * T::BM, n, sl2, qflip);
+        prefill_qtile<D, false>(Qb, Kb, Vb, Ob, lds, u * T::BM, n, qs, ks, sl2, qflip);
     }
 }
 
 template <int D, bool CAUSAL>
 static hipError_t launch_prefill(const PrefillArgs& a) {
     using T = PrefillTile<D>;
-    const int nqt = (int)((a.n + T::BM - 1) / T::BM);
+    const int nqt = (int)((a.n + T::BM - 1) / T::BM);  // a.n: the (longest) sequence length
     const int units = CAUSAL ? (nqt + 1) / 2 : nqt;
     const long long total = (long long)units * a.bh;
     if (total <= 0) return hipSuccess;
-    hipLaunchKernelGGL((flash_prefill_kernel<D, CAUSAL>), dim3((unsigned)total), dim3(T::THREADS), 0,
-                       (hipStream_t)a.stream, (const f16*)a.q, (const f16*)a.k, (const f16*)a.v,
-                       (f16*)a.o, (int)a.n, units, (int)total, a.sl2, a.qflip);
+    const int group = (int)(a.hq / a.hkv);
+    if (a.cu)
+        hipLaunchKernelGGL((flash_prefill_kernel<D, CAUSAL, true>), dim3((unsigned)total), dim3(T::THREADS), 0,
+                           (hipStream_t)a.stream, (const f16*)a.q, (const f16*)a.k, (const f16*)a.v, (f16*)a.o,
+                           a.cu, (int)a.total_rows, (int)a.n, units, (int)total, (int)a.hq, group, a.sl2, a.qflip);
+    else
+        hipLaunchKernelGGL((flash_prefill_kernel<D, CAUSAL, false>), dim3((unsigned)total), dim3(T::THREADS), 0,
+                           (hipStream_t)a.stream, (const f16*)a.q, (const f16*)a.k, (const f16*)a.v, (f16*)a.o,
+                           a.cu, 0, (int)a.n, units, (int)total, (int)a.hq, group, a.sl2, a.qflip);
     return hipGetLastError();
 }
 

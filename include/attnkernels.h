@@ -60,6 +60,31 @@ int ak_flash_wmma(const void *q, const void *k, const void *v, void *o, int64_t 
                   int64_t heads, int64_t seq_len, int64_t head_dim, int causal, double scale,
                   int64_t block_n, void *stream);
 
+/* Prefill with grouped-query attention (GQA/MQA): q, o fp16 [batch, num_heads,
+ * seq_len, head_dim]; k, v fp16 [batch, num_kv_heads, seq_len, head_dim]; query
+ * head h reads kv head h / (num_heads / num_kv_heads).  The same kernel as
+ * ak_flash_wmma; the reference requires num_kv_heads == num_heads
+ * (attnkernels/__init__.py:57-58), where the two agree. */
+int ak_prefill_gqa(const void *q, const void *k, const void *v, void *o, int64_t batch,
+                   int64_t num_heads, int64_t num_kv_heads, int64_t seq_len, int64_t head_dim,
+                   int causal, double scale, void *stream);
+
+/* Prefill over packed variable-length sequences (no padding), GQA allowed.
+ *   q, o: fp16 [total_rows, num_heads, head_dim]; k, v: fp16 [total_rows,
+ *         num_kv_heads, head_dim]; sequence b is rows cu_seqlens[b] ..
+ *         cu_seqlens[b+1] - 1 of all four (self-attention: same lengths for q, k)
+ *   cu_seqlens: int32 [batch + 1], device memory, non-decreasing
+ *   max_seqlen: host value >= every sequence length (it sizes the grid)
+ * Each sequence attends only within itself; causal masks key j > query i of the
+ * same sequence.  Sequence rows are clamped into [0, total_rows): inconsistent
+ * offsets give wrong rows, never an access out of bounds; rows of a sequence
+ * beyond max_seqlen are not written.  The reference's prefill is dense only
+ * (attnkernels/__init__.py:53-61); this is the same kernel on a row-strided layout. */
+int ak_prefill_varlen(const void *q, const void *k, const void *v, void *o,
+                      const int32_t *cu_seqlens, int64_t batch, int64_t total_rows,
+                      int64_t num_heads, int64_t num_kv_heads, int64_t max_seqlen,
+                      int64_t head_dim, int causal, double scale, void *stream);
+
 /* Bytes of device workspace ak_paged_decode needs for these sizes: the fp32
  * split partials o [B, Hq, S, D], m and l [B, Hq, S] with S = ceil(max_context_len /
  * partition), or 0 when S == 1.  Replaces the torch::empty partials of

@@ -249,3 +249,29 @@ def reshape_and_cache(key, value, k_cache, v_cache, slot_mapping):
     kc[slots[ok] // bs, :, slots[ok] % bs, :] = np.asarray(key)[t]
     vc[slots[ok] // bs, :, slots[ok] % bs, :] = np.asarray(value)[t]
     return kc, vc
+
+
+def attention_gqa(q, k, v, causal=False, scale=None):
+    """Attention with grouped kv heads: q [..., H, N, D], k/v [..., H_kv, N, D];
+    query head h reads kv head h // (H / H_kv) (the head map of the reference's
+    decode, paged_decode.cu:68, 183 / reference.py:66-67, applied to prefill)."""
+    q, k, v = np.asarray(q), np.asarray(k), np.asarray(v)
+    g = q.shape[-3] // k.shape[-3]
+    return attention_fp32(q, np.repeat(k, g, axis=-3), np.repeat(v, g, axis=-3), causal, scale)
+
+
+def attention_varlen(q, k, v, cu_seqlens, causal=False, scale=None):
+    """Packed variable-length attention: q [total, H, D], k/v [total, H_kv, D];
+    sequence b is rows cu[b]..cu[b+1]-1 and attends only within itself, each
+    sequence computed as an independent [H, n_b, D] problem with attention_gqa.
+    Returns float32 [total, H, D]."""
+    q, k, v = np.asarray(q), np.asarray(k), np.asarray(v)
+    cu = np.asarray(cu_seqlens, dtype=np.int64)
+    out = np.zeros(q.shape, dtype=np.float32)
+    for b in range(len(cu) - 1):
+        s0, s1 = int(cu[b]), int(cu[b + 1])
+        if s1 > s0:
+            sl = slice(s0, s1)
+            out[sl] = attention_gqa(q[sl].transpose(1, 0, 2), k[sl].transpose(1, 0, 2), v[sl].transpose(1, 0, 2),
+                                    causal, scale).transpose(1, 0, 2)
+    return out

@@ -18,7 +18,7 @@ GOLDEN = Path(__file__).resolve().parent / "golden"
 
 def test_public_surface_matches_reference():
     assert ak.__all__ == ["naive_attention", "flash_attention", "paged_decode", "decode_partition",
-                          "reshape_and_cache", "load_extension"]
+                          "reshape_and_cache", "flash_attention_gqa", "flash_attention_varlen", "load_extension"]
     assert ak.CHUNK == 256 and ak.WMMA_BLOCK_N == {64: 64, 128: 64}
     for name in ("attention_fp32", "make_paged_cache", "gather_kv", "paged_decode_fp32",
                  "paged_decode_torch"):

@@ -33,6 +33,8 @@ def lib():
     L.ak_paged_decode_workspace_size.restype = ctypes.c_size_t
     L.ak_paged_decode.argtypes = [vp] * 6 + [i64] * 8 + [f64, i64, vp, ctypes.c_size_t, vp]
     L.ak_reshape_and_cache.argtypes = [vp] * 5 + [i64] * 7 + [vp]
+    L.ak_prefill_gqa.argtypes = [vp] * 4 + [i64] * 5 + [ctypes.c_int, f64, vp]
+    L.ak_prefill_varlen.argtypes = [vp] * 5 + [i64] * 6 + [ctypes.c_int, f64, vp]
     return L
 
 
@@ -132,3 +134,20 @@ def test_reshape_and_cache_validation(lib):
     # nothing to write: no GPU work, no pointer use
     assert lib.ak_reshape_and_cache(None, None, None, None, None, 0, 8, 128, 10, 16, 1024, 1024, None) == 0
     assert lib.ak_reshape_and_cache(None, None, None, None, None, 4, 8, 128, 0, 16, 1024, 1024, None) == 0
+
+
+def test_gqa_and_varlen_validation(lib):
+    # q, k, v, o, B, H, H_kv, N, D, causal, scale
+    rc = lib.ak_prefill_gqa(FAKE, FAKE, FAKE, FAKE, 1, 6, 4, 16, 64, 0, 0.1, None)
+    assert rc == 1 and b"multiple of num_kv_heads" in lib.ak_last_error()
+    rc = lib.ak_prefill_gqa(FAKE, FAKE, FAKE, FAKE, 1, 8, 2, 16, 96, 0, 0.1, None)
+    assert rc == 2 and b"head_dim must be 64 or 128" in lib.ak_last_error()
+    assert lib.ak_prefill_gqa(None, None, None, None, 0, 8, 2, 16, 64, 0, 0.1, None) == 0
+    # q, k, v, o, cu, B, total, H, H_kv, max_seqlen, D, causal, scale
+    rc = lib.ak_prefill_varlen(FAKE, FAKE, FAKE, FAKE, None, 2, 100, 8, 2, 64, 128, 1, 0.1, None)
+    assert rc == 1 and b"cu_seqlens" in lib.ak_last_error()
+    rc = lib.ak_prefill_varlen(FAKE, FAKE, FAKE, FAKE, ctypes.c_void_p(4098), 2, 100, 8, 2, 64, 128, 1, 0.1, None)
+    assert rc == 1 and b"cu_seqlens" in lib.ak_last_error()
+    rc = lib.ak_prefill_varlen(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 100, 8, 3, 64, 128, 1, 0.1, None)
+    assert rc == 1 and b"multiple of num_kv_heads" in lib.ak_last_error()
+    assert lib.ak_prefill_varlen(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 0, 8, 2, 64, 128, 1, 0.1, None) == 0

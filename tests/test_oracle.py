@@ -332,3 +332,52 @@ def test_planted_writer_mistake_is_caught():
             bad[page, :, row, :] = toks[t]
     got = oracle.gather_kv(bad, bt, bt.shape[1])[0][:, :20]
     assert not np.array_equal(got, toks.transpose(1, 0, 2))
+
+
+# ------------------------------------------------------- GQA / varlen prefill --
+
+@pytest.mark.parametrize("h,hkv", [(4, 4), (8, 2), (6, 1)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_gqa_matches_f64_per_head(h, hkv, causal):
+    q, k, v = rand(2, h, 19, 64), rand(2, hkv, 19, 64), rand(2, hkv, 19, 64)
+    got = oracle.attention_gqa(q, k, v, causal)
+    for head in range(h):
+        want = f64.attention_f64(q[:, head], k[:, head // (h // hkv)], v[:, head // (h // hkv)], causal, None)
+        assert np.abs(got[:, head] - want).max() < 2e-5
+
+
+def test_planted_gqa_head_map_is_caught():
+    """kv head h % H_kv instead of h // G: different for G > 1."""
+    q, k, v = rand(1, 8, 11, 64), rand(1, 2, 11, 64), rand(1, 2, 11, 64)
+    bad = oracle.attention_fp32(q, k[:, [h % 2 for h in range(8)]], v[:, [h % 2 for h in range(8)]], False)
+    assert np.abs(bad - oracle.attention_gqa(q, k, v, False)).max() > 1e-2
+
+
+def test_varlen_single_sequence_equals_dense():
+    q, k, v = rand(40, 4, 64), rand(40, 2, 64), rand(40, 2, 64)
+    got = oracle.attention_varlen(q, k, v, [0, 40], True)
+    dense = oracle.attention_gqa(q.transpose(1, 0, 2), k.transpose(1, 0, 2), v.transpose(1, 0, 2), True)
+    assert np.array_equal(got, dense.transpose(1, 0, 2))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_varlen_matches_f64_per_sequence(causal):
+    cu = [0, 1, 18, 18, 50]  # includes an empty sequence
+    q, k, v = rand(50, 2, 128), rand(50, 2, 128), rand(50, 2, 128)
+    got = oracle.attention_varlen(q, k, v, cu, causal)
+    for b in range(4):
+        s0, s1 = cu[b], cu[b + 1]
+        if s1 > s0:
+            want = f64.attention_f64(q[s0:s1].transpose(1, 0, 2), k[s0:s1].transpose(1, 0, 2),
+                                     v[s0:s1].transpose(1, 0, 2), causal, None)
+            assert np.abs(got[s0:s1] - want.transpose(1, 0, 2)).max() < 2e-5
+
+
+def test_varlen_sequences_are_independent():
+    cu = [0, 30, 70]
+    q, k, v = rand(70, 2, 64), rand(70, 2, 64), rand(70, 2, 64)
+    base = oracle.attention_varlen(q, k, v, cu, False)
+    k2, v2 = k.copy(), v.copy()
+    k2[30:], v2[30:] = rand(40, 2, 64), rand(40, 2, 64)
+    other = oracle.attention_varlen(q, k2, v2, cu, False)
+    assert np.array_equal(base[:30], other[:30]) and not np.array_equal(base[30:], other[30:])
