@@ -377,18 +377,13 @@ flash_prefill_kernel(const f16* __restrict__ Q, const f16* __restrict__ K, const
                      int units_per_bh, int total_units, int hq, int group, float sl2, uint32_t qflip) {
     using T = PrefillTile<D>;
     __shared__ __attribute__((aligned(1024))) f16 lds[2 * T::STAGE];
-    const int L = xcd_remap((int)blockIdx.x, total_units);
-    int bh, u;
-    if (VARLEN) {
-        // Highest units first: only the longest sequences have them, so the
-        // heaviest work starts early and short sequences fill the tail.
-        const int nbh = total_units / units_per_bh;
-        u = units_per_bh - 1 - L / nbh;
-        bh = L - (L / nbh) * nbh;
-    } else {
-        bh = L / units_per_bh;
-        u = L % units_per_bh;
-    }
+    // Dense: every (b, h) has the same units, so contiguous ranges per XCD are
+    // balanced.  Varlen: the units past a short sequence are empty, so whole
+    // GQA groups (all units of the query heads sharing a kv head) are dealt to
+    // the XCDs round-robin instead.
+    const int L = VARLEN ? xcd_chunk_remap((int)blockIdx.x, total_units, units_per_bh * group)
+                         : xcd_remap((int)blockIdx.x, total_units);
+    const int bh = L / units_per_bh, u = L % units_per_bh;
     const int b = bh / hq, h = bh - b * hq, hkv = hq / group, kvh = h / group;
     int n, qs, ks;
     size_t qbase, kvbase;

@@ -80,4 +80,16 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
     return x * per + (x < rem ? x : rem) + slot;
 }
 
+// Remap a linear workgroup id so that logical chunks of `chunk` consecutive
+// tiles go to the XCDs round-robin (chunk j to XCD j % 8), each chunk whole on
+// one XCD: its tiles share that XCD's L2, and every XCD receives a
+// representative mix of chunks even when their costs differ.  A bijection on
+// [0, total): ids past the last full group of 8 chunks map to themselves.
+__device__ __forceinline__ int xcd_chunk_remap(int bid, int total, int chunk) {
+    const int group = kNumXcd * chunk;
+    if (bid >= total / group * group) return bid;
+    const int x = bid % kNumXcd, slot = bid / kNumXcd;
+    return slot / chunk * group + x * chunk + slot % chunk;
+}
+
 }  // namespace ak
