@@ -12,25 +12,30 @@
 // The kernel is built for HBM bandwidth, with no matrix cores:
 //   * a token row of one page is D*2 contiguous bytes; D/8 lanes cover it with
 //     one 16-byte load each, so one wave-wide load reads 4 (D=128) or 8 (D=64)
-//     tokens = 1 KB, and each lane keeps 8 K loads and 8 V loads in flight;
+//     tokens = 1 KB; a D=128 lane keeps 16 K loads and 16 V loads in flight (4
+//     waves per workgroup; 8 and 8 with more than 2 query heads per kv head), a
+//     D=64 lane 4 and 4 (8 waves): the fastest shape of each head size on
+//     ragged and long-context paged caches, as measured on MI355X;
 //   * the dot product is v_dot2_f32_f16 on the raw fp16 q and k, reduced over
 //     the D/8 lanes of a token with DPP row permutes, then scaled by
 //     scale*log2(e) in fp32;
 //   * each group of D/8 lanes runs its own online softmax over the tokens it
 //     loads (no cross-lane traffic in the loop); the groups of a wave and the
-//     4 waves of a workgroup are merged once, at the end, by the same LSE rule.
+//     waves of a workgroup are merged once, at the end, by the same LSE rule.
 #include "attn_kernels.hpp"
 #include "wave.hpp"
 
 namespace ak {
 
-template <int D>
+template <int D, int G>
 struct DecodeTile {
-    static constexpr int NW = 4;                // waves per workgroup
-    static constexpr int THREADS = NW * kWave;  // 256
-    static constexpr int LPT = D / 8;           // lanes per token row
-    static constexpr int TPL = kWave / LPT;     // tokens per wave-wide load
-    static constexpr int U = 8;                 // loads in flight per lane, per cache
+    static constexpr int NW = D == 128 ? 4 : 8;  // waves per workgroup
+    static constexpr int THREADS = NW * kWave;   // 256 or 512
+    static constexpr int LPT = D / 8;            // lanes per token row
+    static constexpr int TPL = kWave / LPT;      // tokens per wave-wide load
+    // loads in flight per lane, per cache (8 for D=128 with more than 2 query
+    // heads per kv head: their q and accumulators need the registers)
+    static constexpr int U = D == 128 ? (G <= 2 ? 16 : 8) : 4;
     static constexpr int TOK = U * TPL;         // tokens per wave iteration
 };
 
@@ -46,13 +51,13 @@ __device__ __forceinline__ float dot8(f16x8 a, f16x8 b) {
 }
 
 template <int D, int G>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__((DecodeTile<D, G>::THREADS))
 paged_decode_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const f16* __restrict__ vc,
                     const int* __restrict__ block_tables, const int* __restrict__ ctx_lens,
                     f16* __restrict__ out, float* __restrict__ o_part, float* __restrict__ m_part,
                     float* __restrict__ l_part, int hkv, int bs, int bs_shift, int max_blocks,
                     int num_blocks, int partition, int num_splits, float sl2) {
-    using T = DecodeTile<D>;
+    using T = DecodeTile<D, G>;
     __shared__ float red_acc[T::NW][G][D];
     __shared__ float red_m[T::NW][G], red_l[T::NW][G];
 
@@ -266,7 +271,7 @@ paged_reduce_kernel(const float* __restrict__ o_part, const float* __restrict__ 
 
 template <int D, int G>
 static hipError_t launch_decode(const DecodeArgs& a) {
-    using T = DecodeTile<D>;
+    using T = DecodeTile<D, G>;
     int bs_shift = -1;
     for (int s = 0; s < 31; ++s)
         if ((int64_t(1) << s) == a.bs) bs_shift = s;
