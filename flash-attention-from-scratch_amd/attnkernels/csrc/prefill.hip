@@ -94,6 +94,16 @@ __device__ __forceinline__ int v_chunk(int r, int c) {
 // (vmcnt).  Each wave writes LPW contiguous KB of the tile; lane l fills the
 // 16-byte slot l of a KB.  Row r starts r * rs elements after src.  Rows past n
 // are clamped to row n-1: in bounds, and masked to -inf later.
+//
+// The load is issued as inline asm (M0 = LDS destination, set by the operand
+// constraint; s_nop 0 is the one wait state an M0 write needs before an LDS
+// DMA).  Issued through the builtin, the compiler's wait-count model treats the
+// LDS counter as out of order for the whole loop and waits lgkmcnt(0) before
+// every MFMA that reads a K or V fragment; hidden from it, the fragment reads
+// get partial waits.  The compiler then no longer orders anything after these
+// loads: every reader of the tile waits in wait_loads_and_sync (vmcnt(0), then
+// the barrier), and the buffer a load overwrites was last read before the
+// barrier that precedes it.
 template <int D, bool IS_V>
 __device__ __forceinline__ void load_kv(const f16* __restrict__ src, f16* dst, int k0, int n, int rs, int w,
                                         int lane) {
@@ -103,8 +113,9 @@ __device__ __forceinline__ void load_kv(const f16* __restrict__ src, f16* dst, i
         const int blk = w * T::LPW + j;
         const int row = blk * T::RPI + lane / T::CPR, p = lane % T::CPR;
         const int c = IS_V ? v_chunk<D>(row, p) : k_chunk<D>(row, p);
-        __builtin_amdgcn_global_load_lds((AK_GLOBAL const void*)(src + (size_t)min(k0 + row, n - 1) * rs + c * 8),
-                                         (AK_LDS void*)(dst + blk * 512), 16, 0, 0);
+        const f16* g = src + (size_t)min(k0 + row, n - 1) * rs + c * 8;
+        const uint32_t l = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(AK_LDS void*)(dst + blk * 512));
+        asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(l));
     }
 }
 
@@ -310,11 +321,15 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
             if constexpr (MASK) mask_tile<D, CAUSAL>(sc, t * T::BN, n, qrow, half);
             max_tile<D>(sc, o, ms_run, l_run, sl2);
         }
+        // The wave holds priority 1 while its QK^T MFMAs and exponentials run and
+        // drops to 0 for P V and the max/barrier phase, so of the two waves on a
+        // SIMD the one in the mixed MFMA+VALU phase issues first.  s_setprio ends
+        // a scheduling region: each phase carries its own interleave.
+        __builtin_amdgcn_s_setprio(1);
         qk_tile<D>(kbuf + ((t + 1) & 1) * T::TILE, qf, sn, lane);
+        f16x8 pf[T::PC];
         if (act) {
-            f16x8 pf[T::PC];
             exp_tile<D>(sc, pf, ms_run, l_run, sl2);
-            pv_tile<D>(vbuf + (t & 1) * T::TILE, pf, o, lane);
             __builtin_amdgcn_sched_group_barrier(0x100, kKPrefetch, 0);
 #pragma unroll
             for (int i = 0; i < T::KB * T::DC; ++i) {
@@ -323,6 +338,12 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
                 __builtin_amdgcn_sched_group_barrier(0x400, kExpPerMfma, 0);  // exp
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // next K fragment read
             }
+        } else {
+            __builtin_amdgcn_sched_group_barrier(0x100, kKPrefetch, 0);
+        }
+        __builtin_amdgcn_s_setprio(0);
+        if (act) {
+            pv_tile<D>(vbuf + (t & 1) * T::TILE, pf, o, lane);
             __builtin_amdgcn_sched_group_barrier(0x100, kVPrefetch, 0);
 #pragma unroll
             for (int i = 0; i < T::DT * T::PC; ++i) {
@@ -330,6 +351,7 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
                 __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // transposed V reads
             }
         }
+        __builtin_amdgcn_s_setprio(0);
     };
     int t = 0;
     for (; t + 1 < kt_mask; t += 2) {
