@@ -257,7 +257,48 @@ def cpu_baseline(seconds):
     flops = oracle.prefill_flops(1, done, n, d, True)
     return dict(value=round(flops / el / 1e12, 5), unit="TFLOP/s", cores=int(threads), kind="port",
                 sample=f"{done} (batch, head) slices of causal N=8192 D=128 through the numpy fp32 "
-                       f"oracle, {el:.1f} s, os.cpu_count()={os.cpu_count()}")
+                       f"oracle, {el:.1f} s, os.cpu_count()={os.cpu_count()}",
+                configs=cpu_configs())
+
+
+def cpu_configs():
+    """The same oracle on the other reference configurations (wall time,
+    time.perf_counter, median of several runs; nothing extrapolated):
+    prefill B=1 H=4 N=256 D=64 and B=4 H=16 N=2048 D=64 (non-causal, scale
+    1/8) whole, and paged decode on the first 8 of the 64 ragged sequences
+    of the decode workload (same seeded lengths, Hq=Hkv=32, D=128, pages of 16)."""
+    import statistics
+
+    import numpy as np
+    import torch
+
+    import oracle
+
+    def median_s(fn, runs):
+        ts = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    rng = np.random.default_rng(1)
+    rows = []
+    for (b, h, n, d, runs) in ((1, 4, 256, 64, 5), (4, 16, 2048, 64, 3)):
+        q, k, v = (rng.standard_normal((b, h, n, d), dtype=np.float32).astype(np.float16) for _ in range(3))
+        sec = median_s(lambda: oracle.attention_fp32(q, k, v, False, 0.125), runs)
+        rows.append(dict(config=f"prefill B={b} H={h} N={n} D={d} non-causal",
+                         value=round(oracle.prefill_flops(b, h, n, d, False) / sec / 1e12, 5), unit="TFLOP/s",
+                         seconds=round(sec, 4), runs=runs, stat="median"))
+    lens = torch.randint(1, 4097, (64,), generator=torch.Generator().manual_seed(4)).tolist()[:8]
+    kc, vc, bt, cl = oracle.make_paged_cache(lens, 32, 128, 16, seed=4)
+    qd = rng.standard_normal((len(lens), 32, 128), dtype=np.float32).astype(np.float16)
+    sec = median_s(lambda: oracle.paged_decode_fp32(qd, kc, vc, bt, cl), 3)
+    rows.append(dict(config=f"paged decode, first 8 of the 64 ragged sequences (sum_ctx={sum(lens)}) "
+                            "Hq=Hkv=32 D=128 bs=16",
+                     value=round(oracle.decode_kv_bytes(lens, 32, 128) / sec / 1e9, 3), unit="GB/s",
+                     seconds=round(sec, 4), runs=3, stat="median"))
+    return rows
 
 
 def main():
