@@ -222,6 +222,23 @@ __device__ __forceinline__ void exp_tile(const f32x16 (&s)[PrefillTile<D>::KB], 
     l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
 }
 
+// exp_tile over key steps [C0, C1) with the row-sum chains held by the caller:
+// at D = 64 a tile has twice the scores per MFMA of D = 128, so half of them
+// are exponentiated under the P V MFMAs instead of all under QK^T.
+template <int D, int C0, int C1>
+__device__ __forceinline__ void exp_part(const f32x16 (&s)[PrefillTile<D>::KB], f16x8 (&pf)[PrefillTile<D>::PC],
+                                         float ms_run, float (&ps)[4], float sl2) {
+    const f16x2 ones = {(f16)1.f, (f16)1.f};
+#pragma unroll
+    for (int c = C0; c < C1; ++c) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pf[c][i] = (f16)exp2_fast(fmaf(s[c >> 1][(c & 1) * 8 + i], sl2, -ms_run));
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            ps[i] = __builtin_amdgcn_fdot2(f16x2{pf[c][2 * i], pf[c][2 * i + 1]}, ones, ps[i], false);
+    }
+}
+
 // O^T += V^T P^T.  Transposed reads: in each 16-lane group, lane a points at
 // row kb + a/4, head dims dbase + 4*sw(a%4) (sw swaps bits 0/1); lane i then
 // receives keys kb..kb+3 of head dim dbase + 4*sw(i/4) + i%4.
@@ -250,11 +267,40 @@ __device__ __forceinline__ void pv_tile(const f16* __restrict__ vs, const f16x8 
     }
 }
 
+// pv_tile with the key step outermost: the MFMAs of step c need only pf[c], so
+// the exponentials of later steps can run under the MFMAs of earlier ones.
+template <int D>
+__device__ __forceinline__ void pv_tile_kmajor(const f16* __restrict__ vs, const f16x8 (&pf)[PrefillTile<D>::PC],
+                                               f32x16 (&o)[PrefillTile<D>::DT], int lane) {
+    using T = PrefillTile<D>;
+    const int half = lane >> 5, a = lane & 15, gd = (lane >> 4) & 1;
+    const int dsub = 16 * gd + 4 * (((a & 1) << 1) | ((a >> 1) & 1));
+#pragma unroll
+    for (int c = 0; c < T::PC; ++c) {
+#pragma unroll
+        for (int t = 0; t < T::DT; ++t) {
+            const int dcol = t * 32 + dsub;
+            f16x4 lohi[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int r = 16 * c + 8 * e + 4 * half + (a >> 2);
+                const f16* p = vs + r * D + v_chunk<D>(r, dcol >> 3) * 8 + (dcol & 7);
+                lohi[e] = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((AK_LDS s16x4*)p));
+            }
+            const f16x8 va = {lohi[0][0], lohi[0][1], lohi[0][2], lohi[0][3],
+                              lohi[1][0], lohi[1][1], lohi[1][2], lohi[1][3]};
+            o[t] = mfma32x32x16(va, pf[c], o[t]);
+        }
+    }
+}
+
 // Instruction interleave of one pipelined tile (sched_group_barrier masks:
 // 0x008 MFMA, 0x002 VALU, 0x400 transcendental, 0x100 LDS read).  Per MFMA of
 // the next tile's S: a few VALU ops and exponentials of this tile's P and the
 // K read for a later MFMA; K reads run kKPrefetch ahead, V reads kVPrefetch.
-constexpr int kValuPerMfma = 3, kExpPerMfma = 2, kKPrefetch = 2, kVPrefetch = 4;
+// At D = 64 each P V MFMA also takes kValuPerPvMfma VALU ops and kExpPerMfma
+// exponentials of the second half of P.
+constexpr int kValuPerMfma = 3, kExpPerMfma = 2, kKPrefetch = 2, kVPrefetch = 4, kValuPerPvMfma = 4;
 
 // Software-pipelined key loop: iteration t multiplies the scores of tile t
 // (computed one iteration earlier) into O while the matrix core computes the
@@ -328,8 +374,10 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
         __builtin_amdgcn_s_setprio(1);
         qk_tile<D>(kbuf + ((t + 1) & 1) * T::TILE, qf, sn, lane);
         f16x8 pf[T::PC];
+        float ps[4] = {0.f, 0.f, 0.f, 0.f};
         if (act) {
-            exp_tile<D>(sc, pf, ms_run, l_run, sl2);
+            if constexpr (D == 64) exp_part<D, 0, T::PC / 2>(sc, pf, ms_run, ps, sl2);
+            else exp_tile<D>(sc, pf, ms_run, l_run, sl2);
             __builtin_amdgcn_sched_group_barrier(0x100, kKPrefetch, 0);
 #pragma unroll
             for (int i = 0; i < T::KB * T::DC; ++i) {
@@ -343,12 +391,22 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
         }
         __builtin_amdgcn_s_setprio(0);
         if (act) {
-            pv_tile<D>(vbuf + (t & 1) * T::TILE, pf, o, lane);
+            if constexpr (D == 64) {
+                exp_part<D, T::PC / 2, T::PC>(sc, pf, ms_run, ps, sl2);
+                l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+                pv_tile_kmajor<D>(vbuf + (t & 1) * T::TILE, pf, o, lane);
+            } else {
+                pv_tile<D>(vbuf + (t & 1) * T::TILE, pf, o, lane);
+            }
             __builtin_amdgcn_sched_group_barrier(0x100, kVPrefetch, 0);
 #pragma unroll
             for (int i = 0; i < T::DT * T::PC; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (O += V^T P^T)
                 __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // transposed V reads
+                if constexpr (D == 64) {
+                    __builtin_amdgcn_sched_group_barrier(0x002, kValuPerPvMfma, 0);  // second half of P
+                    __builtin_amdgcn_sched_group_barrier(0x400, kExpPerMfma, 0);
+                }
             }
         }
         __builtin_amdgcn_s_setprio(0);
