@@ -46,8 +46,9 @@ int prefill(const char* who, const void* q, const void* k, const void* v, void* 
     if (!q || !k || !v || !o) return fail(AK_ERR_INVALID_ARGUMENT, std::string(who) + ": null pointer");
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
         return fail(AK_ERR_INVALID_ARGUMENT, std::string(who) + ": pointers must be 16-byte aligned");
-    // Workgroups = query-tile units (256 rows, causal: pairs) x batch x heads: an int.
-    const int64_t tiles = (seq_len + 255) / 256, units = causal ? (tiles + 1) / 2 : tiles;
+    // Workgroups = query-tile units (128 or 256 rows, causal: pairs) x batch x
+    // heads: an int, counted here for the smaller tile.
+    const int64_t tiles = (seq_len + 127) / 128, units = causal ? (tiles + 1) / 2 : tiles;
     if (seq_len > INT_MAX / 2 || total_rows > INT_MAX / 2 || batch * heads > INT_MAX / units)
         return fail(AK_ERR_INVALID_ARGUMENT, std::string(who) + ": size out of range");
     ak::PrefillArgs a{};

@@ -10,7 +10,8 @@
 //     each wave owns 32 of them, so no softmax row is shared between waves.
 //     Eight waves share each K/V tile in LDS: half the LDS traffic per query
 //     row of a 4-wave workgroup, and each wave issues only 2 one-KB loads per
-//     K and per V tile.
+//     K and per V tile.  Short sequences and small grids use 4-wave workgroups
+//     (128 rows, two per CU) instead: see prefill_waves.
 //   * Scores are computed transposed, S^T = K Q^T, with K as the MFMA A operand
 //     (16-byte LDS reads of K rows) and Q as the B operand (kept in VGPRs for
 //     the whole kernel).  In the accumulator a lane then holds one query column
@@ -30,7 +31,7 @@
 //     16-byte chunks are XOR-swizzled by row so that the K operand reads, the
 //     transposed V reads and the DMA writes are all free of bank conflicts.
 //     64 KB per workgroup.  At about 230 VGPRs a SIMD holds two waves, so a CU
-//     runs one 8-wave workgroup at a time.
+//     runs one 8-wave workgroup, or two 4-wave workgroups, at a time.
 //   * The key loop is software-pipelined inside each wave: while the matrix
 //     core computes the scores of tile t+1, the VALU turns the scores of tile
 //     t into P (exponentials, fp16 conversion, row sums), then P V of tile t
@@ -53,10 +54,10 @@ namespace ak {
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
-template <int D>
+template <int D, int NWAVES = 8>
 struct PrefillTile {
-    static constexpr int NW = 8;                 // waves per workgroup
-    static constexpr int THREADS = NW * kWave;   // 512
+    static constexpr int NW = NWAVES;            // waves per workgroup: 8, or 4 for short sequences
+    static constexpr int THREADS = NW * kWave;   // 512 or 256
     static constexpr int QW = 32;                // query rows per wave
     static constexpr int BM = NW * QW;           // query rows per workgroup
     static constexpr int CPR = D / 8;            // 16-byte chunks per K/V row
@@ -104,10 +105,10 @@ __device__ __forceinline__ int v_chunk(int r, int c) {
 // loads: every reader of the tile waits in wait_loads_and_sync (vmcnt(0), then
 // the barrier), and the buffer a load overwrites was last read before the
 // barrier that precedes it.
-template <int D, bool IS_V>
+template <int D, bool IS_V, int NW>
 __device__ __forceinline__ void load_kv(const f16* __restrict__ src, f16* dst, int k0, int n, int rs, int w,
                                         int lane) {
-    using T = PrefillTile<D>;
+    using T = PrefillTile<D, NW>;
 #pragma unroll
     for (int j = 0; j < T::LPW; ++j) {
         const int blk = w * T::LPW + j;
@@ -307,12 +308,12 @@ constexpr int kValuPerMfma = 3, kExpPerMfma = 2, kKPrefetch = 2, kVPrefetch = 4,
 // scores of tile t+1, so the exponentials of one tile overlap the QK^T MFMAs
 // of the next inside every wave.  K runs two tiles ahead in a 2-buffer ring,
 // V one tile ahead in another; one barrier per tile.
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, int NW>
 __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const f16* __restrict__ kb,
                                               const f16* __restrict__ vb, f16* __restrict__ ob,
                                               f16* __restrict__ lds, int q0, int n, int qs, int ks, float sl2,
                                               uint32_t qflip) {
-    using T = PrefillTile<D>;
+    using T = PrefillTile<D, NW>;
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = uniform(tid >> 6);
     const int col = lane & 31, half = lane >> 5;
@@ -327,9 +328,9 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
     // their keys are < n and (causal) <= the workgroup's first query row.
     const int kt_mask = min(nkt, CAUSAL ? q0 / T::BN : n / T::BN);
 
-    load_kv<D, false>(kb, kbuf, 0, n, ks, w, lane);
-    load_kv<D, true>(vb, vbuf, 0, n, ks, w, lane);
-    if (nkt > 1) load_kv<D, false>(kb, kbuf + T::TILE, T::BN, n, ks, w, lane);
+    load_kv<D, false, NW>(kb, kbuf, 0, n, ks, w, lane);
+    load_kv<D, true, NW>(vb, vbuf, 0, n, ks, w, lane);
+    if (nkt > 1) load_kv<D, false, NW>(kb, kbuf + T::TILE, T::BN, n, ks, w, lane);
 
     // Q as the MFMA B operand: col = query, k = head dim 16*dc + 8*half .. +7.
     f16x8 qf[T::DC];
@@ -359,8 +360,8 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
     auto body = [&](int t, f32x16 (&sc)[T::KB], f32x16 (&sn)[T::KB], auto mask_tag) {
         constexpr bool MASK = decltype(mask_tag)::value;
         wait_loads_and_sync();  // K(t+1), V(t) landed; nobody reads K(t), V(t-1) any more
-        if (t + 2 < nkt) load_kv<D, false>(kb, kbuf + (t & 1) * T::TILE, (t + 2) * T::BN, n, ks, w, lane);
-        if (t + 1 < nkt) load_kv<D, true>(vb, vbuf + ((t + 1) & 1) * T::TILE, (t + 1) * T::BN, n, ks, w, lane);
+        if (t + 2 < nkt) load_kv<D, false, NW>(kb, kbuf + (t & 1) * T::TILE, (t + 2) * T::BN, n, ks, w, lane);
+        if (t + 1 < nkt) load_kv<D, true, NW>(vb, vbuf + ((t + 1) & 1) * T::TILE, (t + 1) * T::BN, n, ks, w, lane);
         // Causal: a tile whose first key is after this wave's last row is skipped.
         const bool act = !MASK || !CAUSAL || t * T::BN <= qw0 + T::QW - 1;
         if (act) {
@@ -450,12 +451,12 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
 // Packed layout (VARLEN): q/o [total, Hq, D], k/v [total, Hkv, D], sequence b
 // being rows cu[b] .. cu[b+1]-1; the grid is sized for the longest sequence and
 // the units past a shorter one exit before touching memory.
-template <int D, bool CAUSAL, bool VARLEN>
-__global__ void __launch_bounds__(PrefillTile<D>::THREADS) __attribute__((amdgpu_waves_per_eu(2)))
+template <int D, bool CAUSAL, bool VARLEN, int NW>
+__global__ void __launch_bounds__((PrefillTile<D, NW>::THREADS)) __attribute__((amdgpu_waves_per_eu(2)))
 flash_prefill_kernel(const f16* __restrict__ Q, const f16* __restrict__ K, const f16* __restrict__ V,
                      f16* __restrict__ O, const int32_t* __restrict__ cu, int total_rows, int n_max,
                      int units_per_bh, int total_units, int hq, int group, float sl2, uint32_t qflip) {
-    using T = PrefillTile<D>;
+    using T = PrefillTile<D, NW>;
     __shared__ __attribute__((aligned(1024))) f16 lds[2 * T::STAGE];
     // Dense: every (b, h) has the same units, so contiguous ranges per XCD are
     // balanced.  Varlen: the units past a short sequence are empty, so whole
@@ -489,33 +490,53 @@ flash_prefill_kernel(const f16* __restrict__ Q, const f16* __restrict__ K, const
     if (CAUSAL) {
         // Pair the heaviest remaining tile with the lightest: equal work per workgroup.
         const int heavy = nqt - 1 - u;
-        prefill_qtile<D, true>(Qb, Kb, Vb, Ob, lds, heavy * T::BM, n, qs, ks, sl2, qflip);
+        prefill_qtile<D, true, NW>(Qb, Kb, Vb, Ob, lds, heavy * T::BM, n, qs, ks, sl2, qflip);
         if (u != heavy) {
             __syncthreads();  // every wave is done with the buffers before they are refilled
-            prefill_qtile<D, true>(Qb, Kb, Vb, Ob, lds, u * T::BM, n, qs, ks, sl2, qflip);
+            prefill_qtile<D, true, NW>(Qb, Kb, Vb, Ob, lds, u * T::BM, n, qs, ks, sl2, qflip);
         }
     } else {
-        prefill_qtile<D, false>(Qb, Kb, Vb, Ob, lds, u * T::BM, n, qs, ks, sl2, qflip);
+        prefill_qtile<D, false, NW>(Qb, Kb, Vb, Ob, lds, u * T::BM, n, qs, ks, sl2, qflip);
     }
 }
 
-template <int D, bool CAUSAL>
-static hipError_t launch_prefill(const PrefillArgs& a) {
-    using T = PrefillTile<D>;
+template <int D, bool CAUSAL, int NW>
+static hipError_t launch_prefill_nw(const PrefillArgs& a) {
+    using T = PrefillTile<D, NW>;
     const int nqt = (int)((a.n + T::BM - 1) / T::BM);  // a.n: the (longest) sequence length
     const int units = CAUSAL ? (nqt + 1) / 2 : nqt;
     const long long total = (long long)units * a.bh;
     if (total <= 0) return hipSuccess;
     const int group = (int)(a.hq / a.hkv);
     if (a.cu)
-        hipLaunchKernelGGL((flash_prefill_kernel<D, CAUSAL, true>), dim3((unsigned)total), dim3(T::THREADS), 0,
+        hipLaunchKernelGGL((flash_prefill_kernel<D, CAUSAL, true, NW>), dim3((unsigned)total), dim3(T::THREADS), 0,
                            (hipStream_t)a.stream, (const f16*)a.q, (const f16*)a.k, (const f16*)a.v, (f16*)a.o,
                            a.cu, (int)a.total_rows, (int)a.n, units, (int)total, (int)a.hq, group, a.sl2, a.qflip);
     else
-        hipLaunchKernelGGL((flash_prefill_kernel<D, CAUSAL, false>), dim3((unsigned)total), dim3(T::THREADS), 0,
+        hipLaunchKernelGGL((flash_prefill_kernel<D, CAUSAL, false, NW>), dim3((unsigned)total), dim3(T::THREADS), 0,
                            (hipStream_t)a.stream, (const f16*)a.q, (const f16*)a.k, (const f16*)a.v, (f16*)a.o,
                            a.cu, 0, (int)a.n, units, (int)total, (int)a.hq, group, a.sl2, a.qflip);
     return hipGetLastError();
+}
+
+// Workgroup size.  8 waves (256 rows) share each K/V tile among more rows and
+// win on long sequences; 4 waves (128 rows, two workgroups per CU) halve the
+// diagonal band a causal workgroup pays in full and double the workgroup count,
+// which wins on short sequences and small grids.  Measured crossovers on
+// MI355X: causal up to N = 2048 (+25% at 512, +5% at 2048, -4% at 8192),
+// non-causal up to N = 1024 (+10% at 512, 0..+2% at 1024, -3..-6% beyond), and
+// any grid of fewer 8-wave workgroups than half the CUs.
+static int prefill_waves(int64_t n, bool causal, int64_t bh) {
+    const int64_t nqt8 = (n + 255) / 256;
+    const int64_t wg8 = (causal ? (nqt8 + 1) / 2 : nqt8) * bh;
+    if (n <= (causal ? 2048 : 1024) || wg8 < 128) return 4;
+    return 8;
+}
+
+template <int D, bool CAUSAL>
+static hipError_t launch_prefill(const PrefillArgs& a) {
+    return prefill_waves(a.n, CAUSAL, a.bh) == 4 ? launch_prefill_nw<D, CAUSAL, 4>(a)
+                                                 : launch_prefill_nw<D, CAUSAL, 8>(a);
 }
 
 hipError_t prefill_launch(const PrefillArgs& a) {

@@ -119,6 +119,21 @@ def test_non_contiguous_inputs_are_accepted():
     assert max_err(out, oracle.attention_fp32(q.numpy(), k.numpy(), v.numpy(), True)) < TOL[64]
 
 
+@pytest.mark.parametrize("causal,n", [(False, 1100), (True, 2100)])
+@pytest.mark.parametrize("d", [64, 128])
+def test_workgroup_sizes_agree(causal, n, d):
+    """64 heads fill the GPU and run on 8-wave workgroups (256 query rows); two
+    heads alone form a small grid and run on 4-wave workgroups (128 rows).  Each
+    query row sees the same key tiles in the same order either way, so the two
+    results are bit-identical, and both match the oracle."""
+    q, k, v = rand_qkv(1, 64, n, d, seed=n + d)
+    big = run("wmma64", q, k, v, causal)
+    small = run("wmma64", q[:, :2], k[:, :2], v[:, :2], causal)
+    assert torch.equal(big[:, :2], small)
+    ref = oracle.attention_fp32(q[:, :2].numpy(), k[:, :2].numpy(), v[:, :2].numpy(), causal)
+    assert max_err(small, ref) < TOL[d]
+
+
 # ---------------------------------------------------- BASELINE full sizes --
 
 def _device_qkv(b, h, n, d, seed):
