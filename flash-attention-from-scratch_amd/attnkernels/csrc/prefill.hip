@@ -203,29 +203,12 @@ __device__ __forceinline__ void max_tile(const f32x16 (&s)[PrefillTile<D>::KB], 
     }
 }
 
-// P^T = 2^(S^T sl2 - ms) as the fp16 B operand: k-step c = accumulator regs
-// 8*(c%2).. of block c/2.  The row sum is taken over the same fp16 values the
-// MFMA consumes, two at a time by v_dot2_f32_f16 against (1, 1), in 4 chains.
-template <int D>
-__device__ __forceinline__ void exp_tile(const f32x16 (&s)[PrefillTile<D>::KB], f16x8 (&pf)[PrefillTile<D>::PC],
-                                         float ms_run, float& l_run, float sl2) {
-    using T = PrefillTile<D>;
-    float ps[4] = {0.f, 0.f, 0.f, 0.f};
-    const f16x2 ones = {(f16)1.f, (f16)1.f};
-#pragma unroll
-    for (int c = 0; c < T::PC; ++c) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) pf[c][i] = (f16)exp2_fast(fmaf(s[c >> 1][(c & 1) * 8 + i], sl2, -ms_run));
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            ps[i] = __builtin_amdgcn_fdot2(f16x2{pf[c][2 * i], pf[c][2 * i + 1]}, ones, ps[i], false);
-    }
-    l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
-}
-
-// exp_tile over key steps [C0, C1) with the row-sum chains held by the caller:
-// at D = 64 a tile has twice the scores per MFMA of D = 128, so half of them
-// are exponentiated under the P V MFMAs instead of all under QK^T.
+// P^T = 2^(S^T sl2 - ms) as the fp16 B operand, for key steps [C0, C1): k-step
+// c = accumulator regs 8*(c%2).. of block c/2.  The row sum is taken over the
+// same fp16 values the MFMA consumes, two at a time by v_dot2_f32_f16 against
+// (1, 1), in the caller's 4 chains.  D = 64 splits a tile's steps in two: it
+// has twice the scores per MFMA of D = 128, so half of them are exponentiated
+// under the P V MFMAs instead of all under QK^T.
 template <int D, int C0, int C1>
 __device__ __forceinline__ void exp_part(const f32x16 (&s)[PrefillTile<D>::KB], f16x8 (&pf)[PrefillTile<D>::PC],
                                          float ms_run, float (&ps)[4], float sl2) {
@@ -238,6 +221,38 @@ __device__ __forceinline__ void exp_part(const f32x16 (&s)[PrefillTile<D>::KB], 
         for (int i = 0; i < 4; ++i)
             ps[i] = __builtin_amdgcn_fdot2(f16x2{pf[c][2 * i], pf[c][2 * i + 1]}, ones, ps[i], false);
     }
+}
+
+// D = 128 checks the exponents after the fact instead of taking the tile
+// maximum first: P = 2^(S sl2 - m) is computed against the current subtracted
+// maximum m, and only if a lane's tile sum reaches 2^14 (some P near the top of
+// fp16) or is not finite (the first tile, against m = -inf) does the wave come
+// here.  Both lanes of each such row then move m to the row maximum, rescale O
+// and l, and recompute P; rows that do not move recompute the same P.  This
+// saves the row-max pass (16 v_max3, a lane exchange and a compare per tile).
+constexpr float kTileSumLimit = 16384.f;
+template <int D>
+__device__ __forceinline__ void settle_tile(const f32x16 (&s)[PrefillTile<D>::KB], f16x8 (&pf)[PrefillTile<D>::PC],
+                                            f32x16 (&o)[PrefillTile<D>::DT], float& ms_run, float& l_run,
+                                            float& l_tile, bool bad, float sl2) {
+    using T = PrefillTile<D>;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < T::KB; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
+    const float mxs = pair_max(mx) * sl2;
+    const bool move = pair_max(bad ? 1.f : 0.f) > 0.f && mxs > ms_run;
+    if (move) {
+        const float alpha = exp2_fast(ms_run - mxs);  // 0 on the first tile
+        ms_run = mxs;
+        l_run *= alpha;
+#pragma unroll
+        for (int t = 0; t < T::DT; ++t) o[t] *= alpha;
+    }
+    float ps[4] = {0.f, 0.f, 0.f, 0.f};
+    exp_part<D, 0, T::PC>(s, pf, ms_run, ps, sl2);
+    l_tile = (ps[0] + ps[1]) + (ps[2] + ps[3]);
 }
 
 // O^T += V^T P^T.  Transposed reads: in each 16-lane group, lane a points at
@@ -366,7 +381,7 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
         const bool act = !MASK || !CAUSAL || t * T::BN <= qw0 + T::QW - 1;
         if (act) {
             if constexpr (MASK) mask_tile<D, CAUSAL>(sc, t * T::BN, n, qrow, half);
-            max_tile<D>(sc, o, ms_run, l_run, sl2);
+            if constexpr (D == 64) max_tile<D>(sc, o, ms_run, l_run, sl2);  // D = 128: settle_tile
         }
         // The wave holds priority 1 while its QK^T MFMAs and exponentials run and
         // drops to 0 for P V and the max/barrier phase, so of the two waves on a
@@ -378,7 +393,7 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
         float ps[4] = {0.f, 0.f, 0.f, 0.f};
         if (act) {
             if constexpr (D == 64) exp_part<D, 0, T::PC / 2>(sc, pf, ms_run, ps, sl2);
-            else exp_tile<D>(sc, pf, ms_run, l_run, sl2);
+            else exp_part<D, 0, T::PC>(sc, pf, ms_run, ps, sl2);
             __builtin_amdgcn_sched_group_barrier(0x100, kKPrefetch, 0);
 #pragma unroll
             for (int i = 0; i < T::KB * T::DC; ++i) {
@@ -397,6 +412,10 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
                 l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
                 pv_tile_kmajor<D>(vbuf + (t & 1) * T::TILE, pf, o, lane);
             } else {
+                float l_tile = (ps[0] + ps[1]) + (ps[2] + ps[3]);
+                const bool bad = !(l_tile < kTileSumLimit);
+                if (__builtin_amdgcn_ballot_w64(bad)) settle_tile<D>(sc, pf, o, ms_run, l_run, l_tile, bad, sl2);
+                l_run += l_tile;
                 pv_tile<D>(vbuf + (t & 1) * T::TILE, pf, o, lane);
             }
             __builtin_amdgcn_sched_group_barrier(0x100, kVPrefetch, 0);

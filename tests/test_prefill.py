@@ -73,6 +73,21 @@ def test_large_logits(variant, d):
     assert max_err(out, oracle.attention_fp32(q.numpy(), k.numpy(), v.numpy(), True)) < 2 * TOL[d]
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("d", [64, 128])
+def test_running_max_moves_late(causal, d):
+    """Key j's scores grow with j (K row j scaled by 1 + j/40) and key 650 is 4x
+    larger still: the subtracted maximum must move after the first tile, by
+    small steps and by one very large one (exp would overflow fp16 without it)."""
+    q, k, v = rand_qkv(2, 2, 700, d, seed=11 + d)
+    ramp = 1.0 + torch.arange(700, dtype=torch.float32) / 40.0
+    k = (k.float() * ramp[None, None, :, None]).half()
+    k[:, :, 650] *= 4
+    out = run("wmma64", q, k, v, causal)
+    assert torch.isfinite(out).all()
+    assert max_err(out, oracle.attention_fp32(q.numpy(), k.numpy(), v.numpy(), causal)) < 2 * TOL[d]
+
+
 def test_causal_first_row_is_v0():
     q, k, v = rand_qkv(1, 1, 128, 64, seed=5)
     for name in VARIANTS:
