@@ -77,6 +77,23 @@ def test_varlen_on_equal_lengths_is_the_dense_kernel():
     assert torch.equal(out, pack(dense))
 
 
+@pytest.mark.parametrize("d", [64, 128])
+def test_varlen_gqa_workgroup_sizes_agree(d):
+    """Long sequences over 64 query heads run on 8-wave workgroups; one GQA group
+    alone (8 query heads, 1 kv head) is a small grid and runs on 4-wave ones.  The
+    group's heads must come out bit-identical, and both match the oracle."""
+    lens, h, hkv = [2100, 2500], 64, 8
+    q, k, v, cu = packed(lens, h, hkv, d, seed=d)
+    big = ak.flash_attention_varlen(q.cuda(), k.cuda(), v.cuda(), cu.cuda(), max(lens), causal=True)
+    g = h // hkv
+    small = ak.flash_attention_varlen(q[:, :g].contiguous().cuda(), k[:, :1].contiguous().cuda(),
+                                      v[:, :1].contiguous().cuda(), cu.cuda(), max(lens), causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(big[:, :g], small)
+    want = oracle.attention_varlen(q[:, :g].numpy(), k[:, :1].numpy(), v[:, :1].numpy(), cu.numpy(), True)
+    assert max_err(small, want) < TOL[d]
+
+
 def test_varlen_host_offsets_and_larger_max_seqlen():
     q, k, v, cu = packed([90, 300], 4, 2, 64, seed=20)
     out = ak.flash_attention_varlen(q.cuda(), k.cuda(), v.cuda(), cu, 2048, causal=True)  # host cu, loose max
