@@ -389,7 +389,8 @@ def main():
                      "frac": round(ach / PEAK_FP16_TFLOPS, 4),
                      "traffic": (measured_traffic("prefill_d128_n8192_causal") or {}).get("traffic_bytes"),
                      "traffic_source": "profiles/traffic.json (rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-scaled)",
-                     "kernel": "flash_prefill_kernel<128,true>",
+                     "kernel": (measured_traffic("prefill_d128_n8192_causal") or {}).get("kernel",
+                                                                                       "flash_prefill_kernel"),
                      "kernel_ms_mean": headline["kernel_ms_mean"]},
         "cpu_baseline": cpu,
         "workloads": workloads,
