@@ -110,11 +110,13 @@ def test_errors_match_reference():
 
 # ------------------------------------------------ bit-exact page gathering --
 
-@pytest.mark.parametrize("d,bs", [(128, 16), (64, 8), (128, 32)])
-def test_gather_reads_exact_token(d, bs):
+@pytest.mark.parametrize("d,bs,group", [(128, 16, 1), (64, 8, 1), (128, 32, 1), (128, 16, 4), (64, 16, 8)])
+def test_gather_reads_exact_token(d, bs, group):
     """Each (sequence, kv head) attends to one chosen token only (its key gets a
     +64 score, every other key -64, scale 1): the output must be that token's V
-    row, bit for bit, which proves the page/offset arithmetic for that token."""
+    row, bit for bit, which proves the page/offset arithmetic for that token.
+    With head groups (16-token pages) this runs the whole-page load path; every
+    query head of a group must return its kv head's chosen row."""
     lens = [1, 16, 17, 255, 256, 513, 1000, 4095]
     hkv = 8
     kc, vc, bt, cl = cache(lens, hkv, d, bs, extra=7, seed=21)
@@ -122,7 +124,7 @@ def test_gather_reads_exact_token(d, bs):
     for trial in range(3):
         k2 = np.zeros_like(kc)
         k2[..., 0] = -8.0
-        q = np.zeros((len(lens), hkv, d), np.float16)
+        q = np.zeros((len(lens), hkv * group, d), np.float16)
         q[..., 0] = 8.0
         chosen = np.zeros((len(lens), hkv), np.int64)
         for b, c in enumerate(lens):
@@ -135,9 +137,9 @@ def test_gather_reads_exact_token(d, bs):
             out = ak.paged_decode(qd, kcd, vcd, btd, cld, max(lens), scale=1.0, partition_size=part)
             got = out.cpu().numpy()
             for b in range(len(lens)):
-                for h in range(hkv):
-                    t = chosen[b, h]
-                    want = vc[bt[b, t // bs], h, t % bs]
+                for h in range(hkv * group):
+                    t = chosen[b, h // group]
+                    want = vc[bt[b, t // bs], h // group, t % bs]
                     assert np.array_equal(got[b, h], want), (trial, part, b, h, t)
 
 
@@ -157,18 +159,24 @@ def test_page_relabelling_is_bit_exact():
         assert torch.equal(a, b), part
 
 
-def test_bad_page_ids_are_not_read():
-    """Out-of-range page ids (undefined in the reference) are skipped, not read."""
-    kc, vc, bt, cl = cache([64], 2, 64, extra=0, seed=41)
+@pytest.mark.parametrize("d,hq,hkv,ctx,bad,bad_id", [(64, 2, 2, 64, [1], 10 ** 6), (128, 8, 2, 600, [5, 21], 10 ** 6),
+                                                      (64, 16, 2, 700, [0, 30], 10 ** 6), (128, 16, 2, 1000, [61], -3)])
+def test_bad_page_ids_are_not_read(d, hq, hkv, ctx, bad, bad_id):
+    """Out-of-range page ids (undefined in the reference; here past the pool or
+    negative) are skipped, not read.  With head groups the bad pages sit inside
+    whole-page chunks, which then hand over to the checked loads."""
+    kc, vc, bt, cl = cache([ctx], hkv, d, extra=0, seed=41)
     bt_bad = bt.copy()
-    bt_bad[0, 1] = 10 ** 6
-    q = rand_q(1, 2, 64, seed=42)
-    out = ak.paged_decode(*to_dev(q, kc, vc, bt_bad, cl), 64, partition_size=256)
-    keep = np.r_[0:16, 32:64]                      # tokens 16..31 sit in the bad page
-    kk = oracle.gather_kv(kc, bt, 4)[0][:, keep]   # [Hkv, 48, D]
-    vv = oracle.gather_kv(vc, bt, 4)[0][:, keep]
-    ref = np.stack([oracle.attention_fp32(q[0, h][None], kk[h], vv[h])[0] for h in range(2)])
-    assert max_err(out[0], ref) < TOL[64]
+    bt_bad[0, bad] = bad_id
+    q = rand_q(1, hq, d, seed=42)
+    nblk = -(-ctx // 16)
+    out = ak.paged_decode(*to_dev(q, kc, vc, bt_bad, cl), ctx, partition_size=256)
+    keep = np.array([t for t in range(ctx) if t // 16 not in bad])
+    kk = oracle.gather_kv(kc, bt, nblk)[0][:, keep]   # [Hkv, kept tokens, D]
+    vv = oracle.gather_kv(vc, bt, nblk)[0][:, keep]
+    g = hq // hkv
+    ref = np.stack([oracle.attention_fp32(q[0, h][None], kk[h // g], vv[h // g])[0] for h in range(hq)])
+    assert max_err(out[0], ref) < TOL[d]
 
 
 # ---------------------------------------------------- BASELINE full sizes --
