@@ -11,7 +11,8 @@
 //     Eight waves share each K/V tile in LDS: half the LDS traffic per query
 //     row of a 4-wave workgroup, and each wave issues only 2 one-KB loads per
 //     K and per V tile.  Short sequences and small grids use 4-wave workgroups
-//     (128 rows, two per CU) instead: see prefill_waves.
+//     (128 rows, two per CU; at D = 64 with 64-key tiles, three per CU)
+//     instead: see prefill_waves.
 //   * Scores are computed transposed, S^T = K Q^T, with K as the MFMA A operand
 //     (16-byte LDS reads of K rows) and Q as the B operand (kept in VGPRs for
 //     the whole kernel).  In the accumulator a lane then holds one query column
@@ -30,8 +31,10 @@
 //     each in a ring of two tiles, one barrier per tile.  Rows are unpadded;
 //     16-byte chunks are XOR-swizzled by row so that the K operand reads, the
 //     transposed V reads and the DMA writes are all free of bank conflicts.
-//     64 KB per workgroup.  At about 230 VGPRs a SIMD holds two waves, so a CU
-//     runs one 8-wave workgroup, or two 4-wave workgroups, at a time.
+//     64 KB per workgroup (32 KB for the 64-key D = 64 tiles).  At about 230
+//     VGPRs a SIMD holds two waves, so a CU runs one 8-wave workgroup, or two
+//     4-wave workgroups, at a time; the D = 64 4-wave kernel stays under 168
+//     VGPRs, and a CU holds three of its workgroups.
 //   * The key loop is software-pipelined inside each wave: while the matrix
 //     core computes the scores of tile t+1, the VALU turns the scores of tile
 //     t into P (exponentials, fp16 conversion, row sums), then P V of tile t
@@ -61,7 +64,11 @@ struct PrefillTile {
     static constexpr int QW = 32;                // query rows per wave
     static constexpr int BM = NW * QW;           // query rows per workgroup
     static constexpr int CPR = D / 8;            // 16-byte chunks per K/V row
-    static constexpr int BN = 8192 / D;          // keys per tile (a K tile is 16 KB): 64 or 128
+    // Keys per tile: a K tile is 16 KB (64 keys at D = 128, 128 at D = 64), except
+    // for D = 64 in 4-wave workgroups, whose 64-key tiles keep the wave under
+    // 168 VGPRs, so that a CU holds three of those workgroups (+5-9% on short
+    // sequences; with 8 waves the 128-key tile is 2-4% faster).
+    static constexpr int BN = D == 64 && NW == 4 ? 64 : 8192 / D;
     static constexpr int TILE = BN * D;          // halves per K (or V) tile
     static constexpr int STAGE = 2 * TILE;       // K + V
     static constexpr int RPI = 512 / D;          // rows per 1 KB load instruction
@@ -150,10 +157,10 @@ constexpr float kRescaleSlack = 8.f;
 
 // S^T = K Q^T for one key tile: KB blocks of 32 keys x 32 queries; lane reads
 // key row 32b+col, chunk 2dc+half.
-template <int D>
-__device__ __forceinline__ void qk_tile(const f16* __restrict__ ks, const f16x8 (&qf)[PrefillTile<D>::DC],
-                                        f32x16 (&s)[PrefillTile<D>::KB], int lane) {
-    using T = PrefillTile<D>;
+template <int D, int NW>
+__device__ __forceinline__ void qk_tile(const f16* __restrict__ ks, const f16x8 (&qf)[(PrefillTile<D, NW>::DC)],
+                                        f32x16 (&s)[(PrefillTile<D, NW>::KB)], int lane) {
+    using T = PrefillTile<D, NW>;
     const int col = lane & 31, half = lane >> 5;
 #pragma unroll
     for (int b = 0; b < T::KB; ++b) {
@@ -168,9 +175,9 @@ __device__ __forceinline__ void qk_tile(const f16* __restrict__ ks, const f16x8 
 }
 
 // Keys past n and, if causal, keys after the query -> -inf.
-template <int D, bool CAUSAL>
-__device__ __forceinline__ void mask_tile(f32x16 (&s)[PrefillTile<D>::KB], int k0, int n, int qrow, int half) {
-    using T = PrefillTile<D>;
+template <int D, int NW, bool CAUSAL>
+__device__ __forceinline__ void mask_tile(f32x16 (&s)[(PrefillTile<D, NW>::KB)], int k0, int n, int qrow, int half) {
+    using T = PrefillTile<D, NW>;
 #pragma unroll
     for (int b = 0; b < T::KB; ++b)
 #pragma unroll
@@ -182,10 +189,10 @@ __device__ __forceinline__ void mask_tile(f32x16 (&s)[PrefillTile<D>::KB], int k
 
 // Tile row maximum; moves the subtracted maximum (and rescales O and l) only
 // when it grows by more than kRescaleSlack, which is rare after the first tile.
-template <int D>
-__device__ __forceinline__ void max_tile(const f32x16 (&s)[PrefillTile<D>::KB], f32x16 (&o)[PrefillTile<D>::DT],
+template <int D, int NW>
+__device__ __forceinline__ void max_tile(const f32x16 (&s)[(PrefillTile<D, NW>::KB)], f32x16 (&o)[(PrefillTile<D, NW>::DT)],
                                          float& ms_run, float& l_run, float sl2) {
-    using T = PrefillTile<D>;
+    using T = PrefillTile<D, NW>;
     float mx = -INFINITY;
 #pragma unroll
     for (int b = 0; b < T::KB; ++b)
@@ -209,8 +216,8 @@ __device__ __forceinline__ void max_tile(const f32x16 (&s)[PrefillTile<D>::KB], 
 // (1, 1), in the caller's 4 chains.  D = 64 splits a tile's steps in two: it
 // has twice the scores per MFMA of D = 128, so half of them are exponentiated
 // under the P V MFMAs instead of all under QK^T.
-template <int D, int C0, int C1>
-__device__ __forceinline__ void exp_part(const f32x16 (&s)[PrefillTile<D>::KB], f16x8 (&pf)[PrefillTile<D>::PC],
+template <int D, int NW, int C0, int C1>
+__device__ __forceinline__ void exp_part(const f32x16 (&s)[(PrefillTile<D, NW>::KB)], f16x8 (&pf)[(PrefillTile<D, NW>::PC)],
                                          float ms_run, float (&ps)[4], float sl2) {
     const f16x2 ones = {(f16)1.f, (f16)1.f};
 #pragma unroll
@@ -231,11 +238,11 @@ __device__ __forceinline__ void exp_part(const f32x16 (&s)[PrefillTile<D>::KB], 
 // and l, and recompute P; rows that do not move recompute the same P.  This
 // saves the row-max pass (16 v_max3, a lane exchange and a compare per tile).
 constexpr float kTileSumLimit = 16384.f;
-template <int D>
-__device__ __forceinline__ void settle_tile(const f32x16 (&s)[PrefillTile<D>::KB], f16x8 (&pf)[PrefillTile<D>::PC],
-                                            f32x16 (&o)[PrefillTile<D>::DT], float& ms_run, float& l_run,
+template <int D, int NW>
+__device__ __forceinline__ void settle_tile(const f32x16 (&s)[(PrefillTile<D, NW>::KB)], f16x8 (&pf)[(PrefillTile<D, NW>::PC)],
+                                            f32x16 (&o)[(PrefillTile<D, NW>::DT)], float& ms_run, float& l_run,
                                             float& l_tile, bool bad, float sl2) {
-    using T = PrefillTile<D>;
+    using T = PrefillTile<D, NW>;
     float mx = -INFINITY;
 #pragma unroll
     for (int b = 0; b < T::KB; ++b)
@@ -251,17 +258,17 @@ __device__ __forceinline__ void settle_tile(const f32x16 (&s)[PrefillTile<D>::KB
         for (int t = 0; t < T::DT; ++t) o[t] *= alpha;
     }
     float ps[4] = {0.f, 0.f, 0.f, 0.f};
-    exp_part<D, 0, T::PC>(s, pf, ms_run, ps, sl2);
+    exp_part<D, NW, 0, T::PC>(s, pf, ms_run, ps, sl2);
     l_tile = (ps[0] + ps[1]) + (ps[2] + ps[3]);
 }
 
 // O^T += V^T P^T.  Transposed reads: in each 16-lane group, lane a points at
 // row kb + a/4, head dims dbase + 4*sw(a%4) (sw swaps bits 0/1); lane i then
 // receives keys kb..kb+3 of head dim dbase + 4*sw(i/4) + i%4.
-template <int D>
-__device__ __forceinline__ void pv_tile(const f16* __restrict__ vs, const f16x8 (&pf)[PrefillTile<D>::PC],
-                                        f32x16 (&o)[PrefillTile<D>::DT], int lane) {
-    using T = PrefillTile<D>;
+template <int D, int NW>
+__device__ __forceinline__ void pv_tile(const f16* __restrict__ vs, const f16x8 (&pf)[(PrefillTile<D, NW>::PC)],
+                                        f32x16 (&o)[(PrefillTile<D, NW>::DT)], int lane) {
+    using T = PrefillTile<D, NW>;
     const int half = lane >> 5, a = lane & 15, gd = (lane >> 4) & 1;
     const int dsub = 16 * gd + 4 * (((a & 1) << 1) | ((a >> 1) & 1));  // within the 32-dim tile
 #pragma unroll
@@ -285,10 +292,10 @@ __device__ __forceinline__ void pv_tile(const f16* __restrict__ vs, const f16x8 
 
 // pv_tile with the key step outermost: the MFMAs of step c need only pf[c], so
 // the exponentials of later steps can run under the MFMAs of earlier ones.
-template <int D>
-__device__ __forceinline__ void pv_tile_kmajor(const f16* __restrict__ vs, const f16x8 (&pf)[PrefillTile<D>::PC],
-                                               f32x16 (&o)[PrefillTile<D>::DT], int lane) {
-    using T = PrefillTile<D>;
+template <int D, int NW>
+__device__ __forceinline__ void pv_tile_kmajor(const f16* __restrict__ vs, const f16x8 (&pf)[(PrefillTile<D, NW>::PC)],
+                                               f32x16 (&o)[(PrefillTile<D, NW>::DT)], int lane) {
+    using T = PrefillTile<D, NW>;
     const int half = lane >> 5, a = lane & 15, gd = (lane >> 4) & 1;
     const int dsub = 16 * gd + 4 * (((a & 1) << 1) | ((a >> 1) & 1));
 #pragma unroll
@@ -368,7 +375,7 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
     wait_loads_and_sync();
     // S(t) alternates between sx and sy (loop unrolled by 2: no copies).
     f32x16 sx[T::KB], sy[T::KB];
-    qk_tile<D>(kbuf, qf, sx, lane);
+    qk_tile<D, NW>(kbuf, qf, sx, lane);
 
     // One tile: sc holds S(t); sn receives S(t+1).  Past the last tile the
     // next K buffer holds stale (in-bounds) data; that S is never used.
@@ -385,20 +392,20 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
         // Causal: a tile whose first key is after this wave's last row is skipped.
         const bool act = !MASK || !CAUSAL || t * T::BN <= qw0 + T::QW - 1;
         if (act) {
-            if constexpr (MASK) mask_tile<D, CAUSAL>(sc, t * T::BN, n, qrow, half);
-            if constexpr (D == 64) max_tile<D>(sc, o, ms_run, l_run, sl2);  // D = 128: settle_tile
+            if constexpr (MASK) mask_tile<D, NW, CAUSAL>(sc, t * T::BN, n, qrow, half);
+            if constexpr (D == 64) max_tile<D, NW>(sc, o, ms_run, l_run, sl2);  // D = 128: settle_tile
         }
         // The wave holds priority 1 while its QK^T MFMAs and exponentials run and
         // drops to 0 for P V and the max/barrier phase, so of the two waves on a
         // SIMD the one in the mixed MFMA+VALU phase issues first.  s_setprio ends
         // a scheduling region: each phase carries its own interleave.
         __builtin_amdgcn_s_setprio(1);
-        qk_tile<D>(kbuf + ((t + 1) & 1) * T::TILE, qf, sn, lane);
+        qk_tile<D, NW>(kbuf + ((t + 1) & 1) * T::TILE, qf, sn, lane);
         f16x8 pf[T::PC];
         float ps[4] = {0.f, 0.f, 0.f, 0.f};
         if (act) {
-            if constexpr (D == 64) exp_part<D, 0, T::PC / 2>(sc, pf, ms_run, ps, sl2);
-            else exp_part<D, 0, T::PC>(sc, pf, ms_run, ps, sl2);
+            if constexpr (D == 64) exp_part<D, NW, 0, T::PC / 2>(sc, pf, ms_run, ps, sl2);
+            else exp_part<D, NW, 0, T::PC>(sc, pf, ms_run, ps, sl2);
             __builtin_amdgcn_sched_group_barrier(0x100, kKPrefetch, 0);
 #pragma unroll
             for (int i = 0; i < T::KB * T::DC; ++i) {
@@ -415,15 +422,15 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
             load_kv<D, true, NW>(vb, vbuf + ((t + 1) & 1) * T::TILE, (t + 1) * T::BN, n, ks, w, lane);
         if (act) {
             if constexpr (D == 64) {
-                exp_part<D, T::PC / 2, T::PC>(sc, pf, ms_run, ps, sl2);
+                exp_part<D, NW, T::PC / 2, T::PC>(sc, pf, ms_run, ps, sl2);
                 l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
-                pv_tile_kmajor<D>(vbuf + (t & 1) * T::TILE, pf, o, lane);
+                pv_tile_kmajor<D, NW>(vbuf + (t & 1) * T::TILE, pf, o, lane);
             } else {
                 float l_tile = (ps[0] + ps[1]) + (ps[2] + ps[3]);
                 const bool bad = !(l_tile < kTileSumLimit);
-                if (__builtin_amdgcn_ballot_w64(bad)) settle_tile<D>(sc, pf, o, ms_run, l_run, l_tile, bad, sl2);
+                if (__builtin_amdgcn_ballot_w64(bad)) settle_tile<D, NW>(sc, pf, o, ms_run, l_run, l_tile, bad, sl2);
                 l_run += l_tile;
-                pv_tile<D>(vbuf + (t & 1) * T::TILE, pf, o, lane);
+                pv_tile<D, NW>(vbuf + (t & 1) * T::TILE, pf, o, lane);
             }
             __builtin_amdgcn_sched_group_barrier(0x100, kVPrefetch, 0);
 #pragma unroll

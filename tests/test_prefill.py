@@ -138,15 +138,21 @@ def test_non_contiguous_inputs_are_accepted():
 @pytest.mark.parametrize("d", [64, 128])
 def test_workgroup_sizes_agree(causal, n, d):
     """64 heads fill the GPU and run on 8-wave workgroups (256 query rows); two
-    heads alone form a small grid and run on 4-wave workgroups (128 rows).  Each
-    query row sees the same key tiles in the same order either way, so the two
-    results are bit-identical, and both match the oracle."""
+    heads alone form a small grid and run on 4-wave workgroups (128 rows).  At
+    D = 128 each query row sees the same 64-key tiles in the same order either
+    way, so the two results are bit-identical.  At D = 64 the 4-wave workgroups
+    take 64-key tiles instead of 128, a different summation order: the results
+    then agree to rounding.  Both match the oracle."""
     q, k, v = rand_qkv(1, 64, n, d, seed=n + d)
     big = run("wmma64", q, k, v, causal)
     small = run("wmma64", q[:, :2], k[:, :2], v[:, :2], causal)
-    assert torch.equal(big[:, :2], small)
+    if d == 128:
+        assert torch.equal(big[:, :2], small)
+    else:
+        assert max_err(big[:, :2], small) < TOL[d]
     ref = oracle.attention_fp32(q[:, :2].numpy(), k[:, :2].numpy(), v[:, :2].numpy(), causal)
     assert max_err(small, ref) < TOL[d]
+    assert max_err(big[:, :2], ref) < TOL[d]
 
 
 # ---------------------------------------------------- BASELINE full sizes --

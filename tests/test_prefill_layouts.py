@@ -80,8 +80,10 @@ def test_varlen_on_equal_lengths_is_the_dense_kernel():
 @pytest.mark.parametrize("d", [64, 128])
 def test_varlen_gqa_workgroup_sizes_agree(d):
     """Long sequences over 64 query heads run on 8-wave workgroups; one GQA group
-    alone (8 query heads, 1 kv head) is a small grid and runs on 4-wave ones.  The
-    group's heads must come out bit-identical, and both match the oracle."""
+    alone (8 query heads, 1 kv head) is a small grid and runs on 4-wave ones.  At
+    D = 128 the group's heads must come out bit-identical; at D = 64 the 4-wave
+    workgroups take 64-key tiles instead of 128 and agree to rounding.  Both
+    match the oracle."""
     lens, h, hkv = [2100, 2500], 64, 8
     q, k, v, cu = packed(lens, h, hkv, d, seed=d)
     big = ak.flash_attention_varlen(q.cuda(), k.cuda(), v.cuda(), cu.cuda(), max(lens), causal=True)
@@ -89,9 +91,13 @@ def test_varlen_gqa_workgroup_sizes_agree(d):
     small = ak.flash_attention_varlen(q[:, :g].contiguous().cuda(), k[:, :1].contiguous().cuda(),
                                       v[:, :1].contiguous().cuda(), cu.cuda(), max(lens), causal=True)
     torch.cuda.synchronize()
-    assert torch.equal(big[:, :g], small)
+    if d == 128:
+        assert torch.equal(big[:, :g], small)
+    else:
+        assert max_err(big[:, :g], small) < TOL[d]
     want = oracle.attention_varlen(q[:, :g].numpy(), k[:, :1].numpy(), v[:, :1].numpy(), cu.numpy(), True)
     assert max_err(small, want) < TOL[d]
+    assert max_err(big[:, :g], want) < TOL[d]
 
 
 def test_varlen_host_offsets_and_larger_max_seqlen():
