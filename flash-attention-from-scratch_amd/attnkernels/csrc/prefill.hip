@@ -189,6 +189,8 @@ __device__ __forceinline__ void mask_tile(f32x16 (&s)[(PrefillTile<D, NW>::KB)],
 
 // Tile row maximum; moves the subtracted maximum (and rescales O and l) only
 // when it grows by more than kRescaleSlack, which is rare after the first tile.
+// Causal D = 64 only: it keeps the 8-wave causal kernel free of spills and the
+// 4-wave one under 168 VGPRs; every other shape checks after the fact.
 template <int D, int NW>
 __device__ __forceinline__ void max_tile(const f32x16 (&s)[(PrefillTile<D, NW>::KB)], f32x16 (&o)[(PrefillTile<D, NW>::DT)],
                                          float& ms_run, float& l_run, float sl2) {
@@ -230,7 +232,8 @@ __device__ __forceinline__ void exp_part(const f32x16 (&s)[(PrefillTile<D, NW>::
     }
 }
 
-// D = 128 checks the exponents after the fact instead of taking the tile
+// D = 128 (and non-causal D = 64, per half tile: settle_part) checks the
+// exponents after the fact instead of taking the tile
 // maximum first: P = 2^(S sl2 - m) is computed against the current subtracted
 // maximum m, and only if a lane's tile sum reaches 2^14 (some P near the top of
 // fp16) or is not finite (the first tile, against m = -inf) does the wave come
@@ -317,6 +320,59 @@ __device__ __forceinline__ void pv_tile_kmajor(const f16* __restrict__ vs, const
     }
 }
 
+// O^T += V^T P^T over key steps [C0, C1), key step outermost.
+template <int D, int NW, int C0, int C1>
+__device__ __forceinline__ void pv_part(const f16* __restrict__ vs, const f16x8 (&pf)[(PrefillTile<D, NW>::PC)],
+                                        f32x16 (&o)[(PrefillTile<D, NW>::DT)], int lane) {
+    using T = PrefillTile<D, NW>;
+    const int half = lane >> 5, a = lane & 15, gd = (lane >> 4) & 1;
+    const int dsub = 16 * gd + 4 * (((a & 1) << 1) | ((a >> 1) & 1));
+#pragma unroll
+    for (int c = C0; c < C1; ++c) {
+#pragma unroll
+        for (int t = 0; t < T::DT; ++t) {
+            const int dcol = t * 32 + dsub;
+            f16x4 lohi[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int r = 16 * c + 8 * e + 4 * half + (a >> 2);
+                const f16* p = vs + r * D + v_chunk<D>(r, dcol >> 3) * 8 + (dcol & 7);
+                lohi[e] = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((AK_LDS s16x4*)p));
+            }
+            const f16x8 va = {lohi[0][0], lohi[0][1], lohi[0][2], lohi[0][3],
+                              lohi[1][0], lohi[1][1], lohi[1][2], lohi[1][3]};
+            o[t] = mfma32x32x16(va, pf[c], o[t]);
+        }
+    }
+}
+
+// One half of P after the fact: as settle_tile, for key steps [C0, C1) only
+// (blocks C0/2 .. C1/2 of S^T), with that half's maximum.  O may already hold
+// the first half's P V: the rescale covers it.
+template <int D, int NW, int C0, int C1>
+__device__ __forceinline__ void settle_part(const f32x16 (&s)[(PrefillTile<D, NW>::KB)],
+                                            f16x8 (&pf)[(PrefillTile<D, NW>::PC)],
+                                            f32x16 (&o)[(PrefillTile<D, NW>::DT)], float& ms_run, float& l_run,
+                                            float& l_part, bool bad, float sl2) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int b = C0 / 2; b < C1 / 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
+    const float mxs = pair_max(mx) * sl2;
+    const bool move = pair_max(bad ? 1.f : 0.f) > 0.f && mxs > ms_run;
+    if (move) {
+        const float alpha = exp2_fast(ms_run - mxs);
+        ms_run = mxs;
+        l_run *= alpha;
+#pragma unroll
+        for (int t = 0; t < PrefillTile<D, NW>::DT; ++t) o[t] *= alpha;
+    }
+    float ps[4] = {0.f, 0.f, 0.f, 0.f};
+    exp_part<D, NW, C0, C1>(s, pf, ms_run, ps, sl2);
+    l_part = (ps[0] + ps[1]) + (ps[2] + ps[3]);
+}
+
 // Instruction interleave of one pipelined tile (sched_group_barrier masks:
 // 0x008 MFMA, 0x002 VALU, 0x400 transcendental, 0x100 LDS read).  Per MFMA of
 // the next tile's S: a few VALU ops and exponentials of this tile's P and the
@@ -391,9 +447,12 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
             load_kv<D, true, NW>(vb, vbuf + ((t + 1) & 1) * T::TILE, (t + 1) * T::BN, n, ks, w, lane);
         // Causal: a tile whose first key is after this wave's last row is skipped.
         const bool act = !MASK || !CAUSAL || t * T::BN <= qw0 + T::QW - 1;
+        // D = 64 with causal masking takes the tile's row maximum first; the other
+        // shapes check the exponents after the fact (settle_tile, settle_part).
+        constexpr bool MAX_FIRST = D == 64 && CAUSAL;
         if (act) {
             if constexpr (MASK) mask_tile<D, NW, CAUSAL>(sc, t * T::BN, n, qrow, half);
-            if constexpr (D == 64) max_tile<D, NW>(sc, o, ms_run, l_run, sl2);  // D = 128: settle_tile
+            if constexpr (MAX_FIRST) max_tile<D, NW>(sc, o, ms_run, l_run, sl2);
         }
         // The wave holds priority 1 while its QK^T MFMAs and exponentials run and
         // drops to 0 for P V and the max/barrier phase, so of the two waves on a
@@ -421,25 +480,60 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
         if (V_LATE && t + 1 < nkt)
             load_kv<D, true, NW>(vb, vbuf + ((t + 1) & 1) * T::TILE, (t + 1) * T::BN, n, ks, w, lane);
         if (act) {
-            if constexpr (D == 64) {
+            if constexpr (MAX_FIRST) {
                 exp_part<D, NW, T::PC / 2, T::PC>(sc, pf, ms_run, ps, sl2);
                 l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
                 pv_tile_kmajor<D, NW>(vbuf + (t & 1) * T::TILE, pf, o, lane);
+                __builtin_amdgcn_sched_group_barrier(0x100, kVPrefetch, 0);
+#pragma unroll
+                for (int i = 0; i < T::DT * T::PC; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (O += V^T P^T)
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // transposed V reads
+                    __builtin_amdgcn_sched_group_barrier(0x002, kValuPerPvMfma, 0);  // second half of P
+                    __builtin_amdgcn_sched_group_barrier(0x400, kExpPerMfma, 0);
+                }
+            } else if constexpr (D == 64) {
+                // Each half of P is checked before its P V MFMAs: the first half was
+                // formed under QK^T, the second is formed under the first half's P V.
+                float l1 = (ps[0] + ps[1]) + (ps[2] + ps[3]);
+                const bool bad1 = !(l1 < kTileSumLimit);
+                if (__builtin_amdgcn_ballot_w64(bad1))
+                    settle_part<D, NW, 0, T::PC / 2>(sc, pf, o, ms_run, l_run, l1, bad1, sl2);
+                l_run += l1;
+                float ps2[4] = {0.f, 0.f, 0.f, 0.f};
+                exp_part<D, NW, T::PC / 2, T::PC>(sc, pf, ms_run, ps2, sl2);
+                pv_part<D, NW, 0, T::PC / 2>(vbuf + (t & 1) * T::TILE, pf, o, lane);
+                __builtin_amdgcn_sched_group_barrier(0x100, kVPrefetch, 0);
+#pragma unroll
+                for (int i = 0; i < T::DT * T::PC / 2; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (first half of P V)
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // transposed V reads
+                    __builtin_amdgcn_sched_group_barrier(0x002, 2 * kValuPerPvMfma, 0);  // second half of P
+                    __builtin_amdgcn_sched_group_barrier(0x400, 2 * kExpPerMfma, 0);
+                }
+                float l2 = (ps2[0] + ps2[1]) + (ps2[2] + ps2[3]);
+                const bool bad2 = !(l2 < kTileSumLimit);
+                if (__builtin_amdgcn_ballot_w64(bad2))
+                    settle_part<D, NW, T::PC / 2, T::PC>(sc, pf, o, ms_run, l_run, l2, bad2, sl2);
+                l_run += l2;
+                pv_part<D, NW, T::PC / 2, T::PC>(vbuf + (t & 1) * T::TILE, pf, o, lane);
+                __builtin_amdgcn_sched_group_barrier(0x100, kVPrefetch, 0);
+#pragma unroll
+                for (int i = 0; i < T::DT * T::PC / 2; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (second half of P V)
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // transposed V reads
+                }
             } else {
                 float l_tile = (ps[0] + ps[1]) + (ps[2] + ps[3]);
                 const bool bad = !(l_tile < kTileSumLimit);
                 if (__builtin_amdgcn_ballot_w64(bad)) settle_tile<D, NW>(sc, pf, o, ms_run, l_run, l_tile, bad, sl2);
                 l_run += l_tile;
                 pv_tile<D, NW>(vbuf + (t & 1) * T::TILE, pf, o, lane);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x100, kVPrefetch, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, kVPrefetch, 0);
 #pragma unroll
-            for (int i = 0; i < T::DT * T::PC; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (O += V^T P^T)
-                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // transposed V reads
-                if constexpr (D == 64) {
-                    __builtin_amdgcn_sched_group_barrier(0x002, kValuPerPvMfma, 0);  // second half of P
-                    __builtin_amdgcn_sched_group_barrier(0x400, kExpPerMfma, 0);
+                for (int i = 0; i < T::DT * T::PC; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (O += V^T P^T)
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // transposed V reads
                 }
             }
         }

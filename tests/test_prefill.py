@@ -73,19 +73,27 @@ def test_large_logits(variant, d):
     assert max_err(out, oracle.attention_fp32(q.numpy(), k.numpy(), v.numpy(), True)) < 2 * TOL[d]
 
 
-@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("causal,b,h,n", [(False, 2, 2, 700), (True, 2, 2, 700), (False, 1, 64, 1100),
+                                          (True, 1, 64, 2100)])
 @pytest.mark.parametrize("d", [64, 128])
-def test_running_max_moves_late(causal, d):
-    """Key j's scores grow with j (K row j scaled by 1 + j/40) and key 650 is 4x
-    larger still: the subtracted maximum must move after the first tile, by
-    small steps and by one very large one (exp would overflow fp16 without it)."""
-    q, k, v = rand_qkv(2, 2, 700, d, seed=11 + d)
-    ramp = 1.0 + torch.arange(700, dtype=torch.float32) / 40.0
+def test_running_max_moves_late(causal, b, h, n, d):
+    """Key j's scores grow with j (K row j scaled by 1 + j/40) and keys 500, 650
+    and 1000 are 3-4x larger still: the subtracted maximum must move after the
+    first tile, by small steps and by very large ones (exp would overflow fp16
+    without them).  Keys 500 and 1000 sit in the second half of their key tile
+    and key 650 in the first, for both tile widths (64 and 128 keys); two heads
+    run on 4-wave workgroups and 64 heads on 8-wave ones."""
+    q, k, v = rand_qkv(b, h, n, d, seed=11 + d)
+    ramp = 1.0 + torch.arange(n, dtype=torch.float32) / 40.0
     k = (k.float() * ramp[None, None, :, None]).half()
-    k[:, :, 650] *= 4
+    for key, f in ((500, 3), (650, 4), (1000, 3)):
+        if key < n:
+            k[:, :, key] *= f
     out = run("wmma64", q, k, v, causal)
     assert torch.isfinite(out).all()
-    assert max_err(out, oracle.attention_fp32(q.numpy(), k.numpy(), v.numpy(), causal)) < 2 * TOL[d]
+    for hi in sorted({0, h - 1}):
+        ref = oracle.attention_fp32(q[:, hi].numpy(), k[:, hi].numpy(), v[:, hi].numpy(), causal)
+        assert max_err(out[:, hi], ref) < 2 * TOL[d], hi
 
 
 def test_causal_first_row_is_v0():
