@@ -78,24 +78,25 @@ def log(msg):
 
 
 def timed_steps(fn, steps, warmup):
-    """W untimed calls, then exactly K calls bracketed by synchronize; per-launch
-    HIP events on the current (launch) stream.  Returns (total_ms, mean_event_ms,
-    median_event_ms)."""
+    """W untimed calls, then exactly K calls bracketed by synchronize, with one
+    HIP event on the current (launch) stream at each step boundary (K+1
+    events): step i lasts from event i to event i+1.  One marker per step, not
+    a start and an end, keeps the events' own cost out of short kernels' times.
+    Returns (total_ms, mean_event_ms, median_event_ms)."""
     import torch
 
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     t0 = time.perf_counter()
+    marks[0].record()
     for i in range(steps):
-        starts[i].record()
         fn()
-        ends[i].record()
+        marks[i + 1].record()
     torch.cuda.synchronize()
     total_ms = (time.perf_counter() - t0) * 1e3
-    ev = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    ev = [a.elapsed_time(b) for a, b in zip(marks[:-1], marks[1:])]
     return total_ms, sum(ev) / len(ev), statistics.median(ev)
 
 
