@@ -163,14 +163,17 @@ __device__ __forceinline__ void qk_tile(const f16* __restrict__ ks, const f16x8 
     using T = PrefillTile<D, NW>;
     const int col = lane & 31, half = lane >> 5;
 #pragma unroll
-    for (int b = 0; b < T::KB; ++b) {
-        s[b] = f32x16{};
-        const int r = b * 32 + col;
-        const f16* krow = ks + r * D;
+    for (int b = 0; b < T::KB; ++b) s[b] = f32x16{};
+    // D = 128: head-dim step outermost, so consecutive MFMAs share the Q operand
+    // and write independent accumulators (+0.5-0.7% at N = 8192, bit-identical);
+    // D = 64 was not faster that way.
+    constexpr bool DC_OUTER = D == 128;
 #pragma unroll
-        for (int dc = 0; dc < T::DC; ++dc)
-            s[b] = mfma32x32x16(*reinterpret_cast<const f16x8*>(krow + k_chunk<D>(r, 2 * dc + half) * 8), qf[dc],
-                                s[b]);
+    for (int x = 0; x < T::KB * T::DC; ++x) {
+        const int b = DC_OUTER ? x % T::KB : x / T::DC, dc = DC_OUTER ? x / T::KB : x % T::DC;
+        const int r = b * 32 + col;
+        s[b] = mfma32x32x16(*reinterpret_cast<const f16x8*>(ks + r * D + k_chunk<D>(r, 2 * dc + half) * 8), qf[dc],
+                            s[b]);
     }
 }
 
@@ -265,36 +268,11 @@ __device__ __forceinline__ void settle_tile(const f32x16 (&s)[(PrefillTile<D, NW
     l_tile = (ps[0] + ps[1]) + (ps[2] + ps[3]);
 }
 
-// O^T += V^T P^T.  Transposed reads: in each 16-lane group, lane a points at
-// row kb + a/4, head dims dbase + 4*sw(a%4) (sw swaps bits 0/1); lane i then
-// receives keys kb..kb+3 of head dim dbase + 4*sw(i/4) + i%4.
-template <int D, int NW>
-__device__ __forceinline__ void pv_tile(const f16* __restrict__ vs, const f16x8 (&pf)[(PrefillTile<D, NW>::PC)],
-                                        f32x16 (&o)[(PrefillTile<D, NW>::DT)], int lane) {
-    using T = PrefillTile<D, NW>;
-    const int half = lane >> 5, a = lane & 15, gd = (lane >> 4) & 1;
-    const int dsub = 16 * gd + 4 * (((a & 1) << 1) | ((a >> 1) & 1));  // within the 32-dim tile
-#pragma unroll
-    for (int t = 0; t < T::DT; ++t) {
-        const int dcol = t * 32 + dsub;
-#pragma unroll
-        for (int c = 0; c < T::PC; ++c) {
-            f16x4 lohi[2];
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const int r = 16 * c + 8 * e + 4 * half + (a >> 2);
-                const f16* p = vs + r * D + v_chunk<D>(r, dcol >> 3) * 8 + (dcol & 7);
-                lohi[e] = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((AK_LDS s16x4*)p));
-            }
-            const f16x8 va = {lohi[0][0], lohi[0][1], lohi[0][2], lohi[0][3],
-                              lohi[1][0], lohi[1][1], lohi[1][2], lohi[1][3]};
-            o[t] = mfma32x32x16(va, pf[c], o[t]);
-        }
-    }
-}
-
-// pv_tile with the key step outermost: the MFMAs of step c need only pf[c], so
-// the exponentials of later steps can run under the MFMAs of earlier ones.
+// O^T += V^T P^T, key step outermost: the MFMAs of step c need only pf[c], so
+// the exponentials of later steps can run under the MFMAs of earlier ones, and
+// consecutive MFMAs share the P operand.  Transposed reads: in each 16-lane
+// group, lane a points at row kb + a/4, head dims dbase + 4*sw(a%4) (sw swaps
+// bits 0/1); lane i then receives keys kb..kb+3 of head dim dbase + 4*sw(i/4) + i%4.
 template <int D, int NW>
 __device__ __forceinline__ void pv_tile_kmajor(const f16* __restrict__ vs, const f16x8 (&pf)[(PrefillTile<D, NW>::PC)],
                                                f32x16 (&o)[(PrefillTile<D, NW>::DT)], int lane) {
@@ -528,7 +506,7 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
                 const bool bad = !(l_tile < kTileSumLimit);
                 if (__builtin_amdgcn_ballot_w64(bad)) settle_tile<D, NW>(sc, pf, o, ms_run, l_run, l_tile, bad, sl2);
                 l_run += l_tile;
-                pv_tile<D, NW>(vbuf + (t & 1) * T::TILE, pf, o, lane);
+                pv_tile_kmajor<D, NW>(vbuf + (t & 1) * T::TILE, pf, o, lane);  // P operand shared by 4 MFMAs
                 __builtin_amdgcn_sched_group_barrier(0x100, kVPrefetch, 0);
 #pragma unroll
                 for (int i = 0; i < T::DT * T::PC; ++i) {
