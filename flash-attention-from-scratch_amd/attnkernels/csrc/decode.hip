@@ -200,8 +200,8 @@ paged_decode_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const
         const int tn = t0 + stride;
         if (tn + T::TOK <= end) load_spages(tn);
         else load_pages(tn, end, pg);
-        const bool all[T::U] = {};
-        consume(kr, vr, all, std::false_type{});
+        const bool unused[T::U] = {};  // unmasked: every token of a whole-page chunk is valid
+        consume(kr, vr, unused, std::false_type{});
         t0 = tn;
     }
     for (; t0 < end; t0 += stride) {
