@@ -340,8 +340,8 @@ def main():
                          "that scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings to bytes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(see DESIGN.md for how the kernels would shard); run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU only: this build has no multi-GPU path; run with --gpus 1.",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
