@@ -200,3 +200,25 @@ def test_baseline_config_properties(cfg):
     o = ak.flash_attention(q, k, v, causal=causal)
     o2 = ak.flash_attention(q, k, v * 2, causal=causal)
     assert (o2.float() - 2 * o.float()).abs().max().item() < 2 * TOL[d]
+
+
+@pytest.mark.parametrize("n", [65536, 100003])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_long_context_rows(n, d, causal):
+    """Beyond the BASELINE sizes: single query rows of a 64k / 100k-token
+    sequence against the oracle over exactly the keys they see (causal: keys
+    0..row), and V = 1 giving O = 1 on every row.  Exercises the row/tile
+    index arithmetic far past 8192 and long running sums."""
+    q, k, v = _device_qkv(1, 2, n, d, seed=13 + n % 7)
+    out = ak.flash_attention(q, k, v, causal=causal)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    hc = 1
+    qs, ks, vs = (t[0, hc].cpu().numpy() for t in (q, k, v))
+    for row in (0, 1, 8191, 8192, n // 2, n - 2, n - 1):
+        lim = row + 1 if causal else n
+        ref = oracle.attention_fp32(qs[row:row + 1], ks[:lim], vs[:lim], False)
+        assert max_err(out[0, hc, row:row + 1], ref) < TOL[d], row
+    o1 = ak.flash_attention(q, k, torch.ones_like(v), causal=causal)
+    assert (o1.float() - 1).abs().max().item() < 2e-3
