@@ -239,3 +239,25 @@ def test_baseline_cfg5_long_context(d):
     ones = torch.ones_like(vcd)
     o1 = ak.paged_decode(qd, kcd, ones, btd, cld, 32768, partition_size=256)
     assert (o1.float() - 1).abs().max().item() < 1e-3
+
+
+@pytest.mark.parametrize("partition", [256, 4096])
+def test_very_long_context_head_groups(partition):
+    """256k and 100001 tokens, 4 query heads per kv head (the whole-page load
+    path), 1024 / 64 splits into the reduce: kv heads 0 and 7 of both sequences
+    against the oracle, gathered through the block table on the device."""
+    lens, hq, hkv, d, bs = [262144, 100001], 32, 8, 128, 16
+    kcd, vcd, bt, cl = baseline_cache(lens, hkv, d, bs, seed=51)
+    q = rand_q(len(lens), hq, d, seed=52)
+    qd, btd, cld = to_dev(q, bt, cl)
+    out = ak.paged_decode(qd, kcd, vcd, btd, cld, max(lens), partition_size=partition)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    g = hq // hkv
+    for b, c in enumerate(lens):
+        pages = torch.from_numpy(bt[b, :-(-c // bs)]).long().cuda()
+        for kvh in (0, hkv - 1):
+            kk = kcd[pages, kvh].reshape(-1, d)[:c].cpu().numpy()
+            vv = vcd[pages, kvh].reshape(-1, d)[:c].cpu().numpy()
+            ref = oracle.attention_fp32(q[b, kvh * g:(kvh + 1) * g], kk, vv, False)
+            assert max_err(out[b, kvh * g:(kvh + 1) * g], ref) < TOL[d], (b, kvh)
