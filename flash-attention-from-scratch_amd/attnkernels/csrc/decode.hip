@@ -121,7 +121,14 @@ paged_decode_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const
     if (fast_bs && start + w * T::TOK + T::TOK <= min(start + partition, max_tok)) load_spages(start + w * T::TOK);
 
     const int ctx = min(ctx_raw, max_tok);
-    if (start >= ctx) return;  // whole workgroup: this split is past the context
+    if (start >= ctx) {  // whole workgroup: this split is past the context
+        // A sequence with no context (outside the >= 1 contract) gets a zero row,
+        // as the reduce gives it when there are several splits.
+        if (num_splits == 1)
+            for (int idx = tid; idx < G * D; idx += T::THREADS)
+                out[((size_t)b * hq + kvh * G + idx / D) * D + idx % D] = (f16)0.f;
+        return;
+    }
     const int end = min(ctx, start + partition);
 
     float m[G], l[G], acc[G][8];

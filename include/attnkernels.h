@@ -98,7 +98,8 @@ size_t ak_paged_decode_workspace_size(int64_t batch, int64_t num_heads, int64_t 
  *   q:            fp16 [batch, num_heads, head_dim], one query token per sequence
  *   k_cache, v_cache: fp16 [num_blocks, num_kv_heads, block_size, head_dim]
  *   block_tables: int32 [batch, max_blocks_per_seq], physical page ids
- *   context_lens: int32 [batch], tokens of context (>= 1) per sequence
+ *   context_lens: int32 [batch], tokens of context (>= 1) per sequence; a
+ *                 sequence with 0 (or less) gets a zero output row
  *   out:          fp16 [batch, num_heads, head_dim]
  *   max_context_len: host value >= every context length
  *   partition:    tokens per split, a positive multiple of 256

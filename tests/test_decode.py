@@ -261,3 +261,20 @@ def test_very_long_context_head_groups(partition):
             vv = vcd[pages, kvh].reshape(-1, d)[:c].cpu().numpy()
             ref = oracle.attention_fp32(q[b, kvh * g:(kvh + 1) * g], kk, vv, False)
             assert max_err(out[b, kvh * g:(kvh + 1) * g], ref) < TOL[d], (b, kvh)
+
+
+@pytest.mark.parametrize("partition", [256, 1 << 20])
+def test_empty_context_gives_zero_rows(partition):
+    """Context length 0 is outside the reference's contract (>= 1); here it
+    yields a zero row with or without split-K, and the other sequences are
+    unaffected."""
+    lens = [0, 300, 0, 17]
+    kc, vc, bt, cl = cache([max(c, 1) for c in lens], 2, 128, seed=61)
+    cl = np.asarray(lens, np.int32)
+    q = rand_q(4, 8, 128, seed=62)
+    out = ak.paged_decode(*to_dev(q, kc, vc, bt, cl), 300, partition_size=partition)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out[[0, 2]]) == 0
+    for b in (1, 3):
+        ref = oracle.paged_decode_fp32(q[b:b + 1], kc, vc, bt[b:b + 1], cl[b:b + 1])
+        assert max_err(out[b:b + 1], ref) < TOL[128], b
