@@ -192,8 +192,7 @@ __device__ __forceinline__ void mask_tile(f32x16 (&s)[(PrefillTile<D, NW>::KB)],
 
 // Tile row maximum; moves the subtracted maximum (and rescales O and l) only
 // when it grows by more than kRescaleSlack, which is rare after the first tile.
-// Causal D = 64 only: it keeps the 8-wave causal kernel free of spills and the
-// 4-wave one under 168 VGPRs; every other shape checks after the fact.
+// Used on the diagonal (masked) tiles of causal D = 64 only.
 template <int D, int NW>
 __device__ __forceinline__ void max_tile(const f32x16 (&s)[(PrefillTile<D, NW>::KB)], f32x16 (&o)[(PrefillTile<D, NW>::DT)],
                                          float& ms_run, float& l_run, float sl2) {
@@ -425,9 +424,11 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
             load_kv<D, true, NW>(vb, vbuf + ((t + 1) & 1) * T::TILE, (t + 1) * T::BN, n, ks, w, lane);
         // Causal: a tile whose first key is after this wave's last row is skipped.
         const bool act = !MASK || !CAUSAL || t * T::BN <= qw0 + T::QW - 1;
-        // D = 64 with causal masking takes the tile's row maximum first; the other
-        // shapes check the exponents after the fact (settle_tile, settle_part).
-        constexpr bool MAX_FIRST = D == 64 && CAUSAL;
+        // The diagonal tiles of causal D = 64 take the tile's row maximum first; all
+        // other tiles check the exponents after the fact (settle_tile, settle_part).
+        // The split check on the masked tiles as well costs the causal D = 64 kernels
+        // their register budget (spills at 8 waves, a third workgroup per CU at 4).
+        constexpr bool MAX_FIRST = D == 64 && CAUSAL && MASK;
         if (act) {
             if constexpr (MASK) mask_tile<D, NW, CAUSAL>(sc, t * T::BN, n, qrow, half);
             if constexpr (MAX_FIRST) max_tile<D, NW>(sc, o, ms_run, l_run, sl2);
