@@ -234,70 +234,12 @@ __device__ __forceinline__ void exp_part(const f32x16 (&s)[(PrefillTile<D, NW>::
     }
 }
 
-// D = 128 (and non-causal D = 64, per half tile: settle_part) checks the
-// exponents after the fact instead of taking the tile
-// maximum first: P = 2^(S sl2 - m) is computed against the current subtracted
-// maximum m, and only if a lane's tile sum reaches 2^14 (some P near the top of
-// fp16) or is not finite (the first tile, against m = -inf) does the wave come
-// here.  Both lanes of each such row then move m to the row maximum, rescale O
-// and l, and recompute P; rows that do not move recompute the same P.  This
-// saves the row-max pass (16 v_max3, a lane exchange and a compare per tile).
-constexpr float kTileSumLimit = 16384.f;
-template <int D, int NW>
-__device__ __forceinline__ void settle_tile(const f32x16 (&s)[(PrefillTile<D, NW>::KB)], f16x8 (&pf)[(PrefillTile<D, NW>::PC)],
-                                            f32x16 (&o)[(PrefillTile<D, NW>::DT)], float& ms_run, float& l_run,
-                                            float& l_tile, bool bad, float sl2) {
-    using T = PrefillTile<D, NW>;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int b = 0; b < T::KB; ++b)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
-    const float mxs = pair_max(mx) * sl2;
-    const bool move = pair_max(bad ? 1.f : 0.f) > 0.f && mxs > ms_run;
-    if (move) {
-        const float alpha = exp2_fast(ms_run - mxs);  // 0 on the first tile
-        ms_run = mxs;
-        l_run *= alpha;
-#pragma unroll
-        for (int t = 0; t < T::DT; ++t) o[t] *= alpha;
-    }
-    float ps[4] = {0.f, 0.f, 0.f, 0.f};
-    exp_part<D, NW, 0, T::PC>(s, pf, ms_run, ps, sl2);
-    l_tile = (ps[0] + ps[1]) + (ps[2] + ps[3]);
-}
-
-// O^T += V^T P^T, key step outermost: the MFMAs of step c need only pf[c], so
-// the exponentials of later steps can run under the MFMAs of earlier ones, and
-// consecutive MFMAs share the P operand.  Transposed reads: in each 16-lane
-// group, lane a points at row kb + a/4, head dims dbase + 4*sw(a%4) (sw swaps
-// bits 0/1); lane i then receives keys kb..kb+3 of head dim dbase + 4*sw(i/4) + i%4.
-template <int D, int NW>
-__device__ __forceinline__ void pv_tile_kmajor(const f16* __restrict__ vs, const f16x8 (&pf)[(PrefillTile<D, NW>::PC)],
-                                               f32x16 (&o)[(PrefillTile<D, NW>::DT)], int lane) {
-    using T = PrefillTile<D, NW>;
-    const int half = lane >> 5, a = lane & 15, gd = (lane >> 4) & 1;
-    const int dsub = 16 * gd + 4 * (((a & 1) << 1) | ((a >> 1) & 1));
-#pragma unroll
-    for (int c = 0; c < T::PC; ++c) {
-#pragma unroll
-        for (int t = 0; t < T::DT; ++t) {
-            const int dcol = t * 32 + dsub;
-            f16x4 lohi[2];
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const int r = 16 * c + 8 * e + 4 * half + (a >> 2);
-                const f16* p = vs + r * D + v_chunk<D>(r, dcol >> 3) * 8 + (dcol & 7);
-                lohi[e] = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((AK_LDS s16x4*)p));
-            }
-            const f16x8 va = {lohi[0][0], lohi[0][1], lohi[0][2], lohi[0][3],
-                              lohi[1][0], lohi[1][1], lohi[1][2], lohi[1][3]};
-            o[t] = mfma32x32x16(va, pf[c], o[t]);
-        }
-    }
-}
-
-// O^T += V^T P^T over key steps [C0, C1), key step outermost.
+// O^T += V^T P^T over key steps [C0, C1), key step outermost: the MFMAs of
+// step c need only pf[c], so the exponentials of later steps can run under the
+// MFMAs of earlier ones, and consecutive MFMAs share the P operand.  Transposed
+// reads: in each 16-lane group, lane a points at row kb + a/4, head dims
+// dbase + 4*sw(a%4) (sw swaps bits 0/1); lane i then receives keys kb..kb+3 of
+// head dim dbase + 4*sw(i/4) + i%4.
 template <int D, int NW, int C0, int C1>
 __device__ __forceinline__ void pv_part(const f16* __restrict__ vs, const f16x8 (&pf)[(PrefillTile<D, NW>::PC)],
                                         f32x16 (&o)[(PrefillTile<D, NW>::DT)], int lane) {
@@ -323,9 +265,17 @@ __device__ __forceinline__ void pv_part(const f16* __restrict__ vs, const f16x8 
     }
 }
 
-// One half of P after the fact: as settle_tile, for key steps [C0, C1) only
-// (blocks C0/2 .. C1/2 of S^T), with that half's maximum.  O may already hold
-// the first half's P V: the rescale covers it.
+// Exponents checked after the fact instead of taking the tile maximum first:
+// P = 2^(S sl2 - m) is computed against the current subtracted maximum m, and
+// only if a lane's sum over key steps [C0, C1) reaches 2^14 (some P near the
+// top of fp16) or is not finite (the first tile, against m = -inf) does the
+// wave come here.  Both lanes of each such row then move m to the maximum of
+// those key steps, rescale O and l, and recompute P for them; rows that do not
+// move recompute the same P.  D = 128 checks whole tiles; D = 64 checks each
+// part of a tile before its P V MFMAs, and when the second part moves m the
+// rescale also covers the first part's P V, already in O.  This saves the
+// row-max pass (v_max3, a lane exchange and a compare per tile).
+constexpr float kTileSumLimit = 16384.f;
 template <int D, int NW, int C0, int C1>
 __device__ __forceinline__ void settle_part(const f32x16 (&s)[(PrefillTile<D, NW>::KB)],
                                             f16x8 (&pf)[(PrefillTile<D, NW>::PC)],
@@ -333,13 +283,13 @@ __device__ __forceinline__ void settle_part(const f32x16 (&s)[(PrefillTile<D, NW
                                             float& l_part, bool bad, float sl2) {
     float mx = -INFINITY;
 #pragma unroll
-    for (int b = C0 / 2; b < C1 / 2; ++b)
+    for (int c = C0; c < C1; ++c)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
+        for (int i = 0; i < 8; ++i) mx = fmaxf(mx, s[c >> 1][(c & 1) * 8 + i]);
     const float mxs = pair_max(mx) * sl2;
     const bool move = pair_max(bad ? 1.f : 0.f) > 0.f && mxs > ms_run;
     if (move) {
-        const float alpha = exp2_fast(ms_run - mxs);
+        const float alpha = exp2_fast(ms_run - mxs);  // 0 on the first tile
         ms_run = mxs;
         l_run *= alpha;
 #pragma unroll
@@ -425,7 +375,7 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
         // Causal: a tile whose first key is after this wave's last row is skipped.
         const bool act = !MASK || !CAUSAL || t * T::BN <= qw0 + T::QW - 1;
         // The diagonal tiles of causal D = 64 take the tile's row maximum first; all
-        // other tiles check the exponents after the fact (settle_tile, settle_part).
+        // other tiles check the exponents after the fact (settle_part).
         // The split check on the masked tiles as well costs the causal D = 64 kernels
         // their register budget (spills at 8 waves, a third workgroup per CU at 4).
         constexpr bool MAX_FIRST = D == 64 && CAUSAL && MASK;
@@ -462,7 +412,7 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
             if constexpr (MAX_FIRST) {
                 exp_part<D, NW, T::PC / 2, T::PC>(sc, pf, ms_run, ps, sl2);
                 l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
-                pv_tile_kmajor<D, NW>(vbuf + (t & 1) * T::TILE, pf, o, lane);
+                pv_part<D, NW, 0, T::PC>(vbuf + (t & 1) * T::TILE, pf, o, lane);
                 __builtin_amdgcn_sched_group_barrier(0x100, kVPrefetch, 0);
 #pragma unroll
                 for (int i = 0; i < T::DT * T::PC; ++i) {
@@ -505,9 +455,10 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
             } else {
                 float l_tile = (ps[0] + ps[1]) + (ps[2] + ps[3]);
                 const bool bad = !(l_tile < kTileSumLimit);
-                if (__builtin_amdgcn_ballot_w64(bad)) settle_tile<D, NW>(sc, pf, o, ms_run, l_run, l_tile, bad, sl2);
+                if (__builtin_amdgcn_ballot_w64(bad))
+                    settle_part<D, NW, 0, T::PC>(sc, pf, o, ms_run, l_run, l_tile, bad, sl2);
                 l_run += l_tile;
-                pv_tile_kmajor<D, NW>(vbuf + (t & 1) * T::TILE, pf, o, lane);  // P operand shared by 4 MFMAs
+                pv_part<D, NW, 0, T::PC>(vbuf + (t & 1) * T::TILE, pf, o, lane);
                 __builtin_amdgcn_sched_group_barrier(0x100, kVPrefetch, 0);
 #pragma unroll
                 for (int i = 0; i < T::DT * T::PC; ++i) {
