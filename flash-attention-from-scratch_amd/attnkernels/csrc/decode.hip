@@ -13,16 +13,17 @@
 //   * a token row of one page is D*2 contiguous bytes; D/8 lanes cover it with
 //     one 16-byte load each, so one wave-wide load reads 4 (D=128) or 8 (D=64)
 //     tokens = 1 KB; a D=128 lane keeps 16 K loads and 16 V loads in flight (4
-//     waves per workgroup; 8 and 8 with more than 2 query heads per kv head), a
-//     D=64 lane 4 and 4 (8 waves): the fastest shape of each head size on
-//     ragged and long-context paged caches, as measured on MI355X;
+//     waves per workgroup; 4 and 4 with 4 query heads per kv head, 8 and 8
+//     with 8), a D=64 lane 4 and 4 (8 waves with one query head per kv head,
+//     4 with head groups): the fastest shape of each head size on ragged and
+//     long-context paged caches, as measured on MI355X;
 //   * the dot product is v_dot2_f32_f16 on the raw fp16 q and k, reduced over
 //     the D/8 lanes of a token with DPP row permutes, then scaled by
 //     scale*log2(e) in fp32;
 //   * each group of D/8 lanes runs its own online softmax over the tokens it
 //     loads (no cross-lane traffic in the loop); the groups of a wave and the
 //     waves of a workgroup are merged once, at the end, by the same LSE rule;
-//   * with head groups and 16-token pages, a wave's chunk is 2 or 4 whole
+//   * with head groups and 16-token pages, a wave's chunk is 1, 2 or 4 whole
 //     pages: their ids are wave-uniform scalar loads and each K/V load is a
 //     page base plus a lane offset plus an immediate, with no per-token page
 //     arithmetic or masking; the context's tail, other page sizes and
@@ -36,13 +37,19 @@ namespace ak {
 
 template <int D, int G>
 struct DecodeTile {
-    static constexpr int NW = D == 128 ? 4 : 8;  // waves per workgroup
+    // Waves per workgroup.  With head groups a workgroup's fixed costs (page
+    // ids, then K/V, before any work; the merge at the end) grow with G while
+    // fewer of them fit on a CU, so D=64 takes 4 waves there: a 256-token
+    // split is then 2 pipelined chunks per wave instead of 1 (1.1-2.1x at the
+    // default partition on MI355X, equal at the best one).
+    static constexpr int NW = D == 128 || G >= 2 ? 4 : 8;
     static constexpr int THREADS = NW * kWave;   // 256 or 512
     static constexpr int LPT = D / 8;            // lanes per token row
     static constexpr int TPL = kWave / LPT;      // tokens per wave-wide load
-    // loads in flight per lane, per cache (8 for D=128 with more than 2 query
-    // heads per kv head: their q and accumulators need the registers)
-    static constexpr int U = D == 128 ? (G <= 2 ? 16 : 8) : 4;
+    // Loads in flight per lane, per cache.  D=128 with head groups spends the
+    // registers on q and the accumulators instead: 8 with 8 query heads per kv
+    // head; 4 with 4, where 115 VGPRs leave 4 waves per SIMD rather than 3.
+    static constexpr int U = D == 128 ? (G <= 2 ? 16 : G == 4 ? 4 : 8) : 4;
     static constexpr int TOK = U * TPL;         // tokens per wave iteration
     // Page size of the fast path: a wave iteration then covers PPI whole pages
     // (its first token is a multiple of TOK, itself a multiple of 16).

@@ -59,6 +59,18 @@ def test_ragged_batch(d, partition):
     assert run(RAGGED, 32, 8, d, partition=partition) < TOL[d]
 
 
+CHUNK_EDGES = [15, 16, 17, 31, 32, 33, 63, 65, 127, 129, 255, 257, 383, 385, 511, 513]
+
+
+@pytest.mark.parametrize("d,hq,hkv", [(128, 16, 4), (128, 64, 8), (64, 8, 4), (64, 32, 4), (64, 64, 8)])
+@pytest.mark.parametrize("partition", [256, 512])
+def test_chunk_edges_head_groups(d, hq, hkv, partition):
+    """Context lengths one token either side of every chunk size the head-group
+    tiles use: 16, 32 or 64 tokens per wave, 64 to 256 per workgroup step; the
+    whole-page loop hands the tail to the checked loop at each of them."""
+    assert run(CHUNK_EDGES, hq, hkv, d, partition=partition) < TOL[d]
+
+
 @pytest.mark.parametrize("bs", [8, 16, 32, 12])
 def test_block_sizes(bs):
     assert run([300, 2000, 17], 8, 2, 128, bs=bs) < TOL[128]
