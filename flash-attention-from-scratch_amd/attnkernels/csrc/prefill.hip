@@ -360,10 +360,10 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
     f32x16 sx[T::KB], sy[T::KB];
     qk_tile<D, NW>(kbuf, qf, sx, lane);
 
-    // One tile: sc holds S(t); sn receives S(t+1).  Past the last tile the
-    // next K buffer holds stale (in-bounds) data; that S is never used.
-    auto body = [&](int t, f32x16 (&sc)[T::KB], f32x16 (&sn)[T::KB], auto mask_tag) {
+    // One tile: sc holds S(t); sn receives S(t+1), which the last tile skips.
+    auto body = [&](int t, f32x16 (&sc)[T::KB], f32x16 (&sn)[T::KB], auto mask_tag, auto last_tag) {
         constexpr bool MASK = decltype(mask_tag)::value;
+        constexpr bool LAST = decltype(last_tag)::value;  // the last tile: no next S to compute
         wait_loads_and_sync();  // K(t+1), V(t) landed; nobody reads K(t), V(t-1) any more
         if (t + 2 < nkt) load_kv<D, false, NW>(kb, kbuf + (t & 1) * T::TILE, (t + 2) * T::BN, n, ks, w, lane);
         // V(t+1) goes to the slot of V(t-1), last read before this barrier.  D = 64
@@ -388,21 +388,23 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
         // SIMD the one in the mixed MFMA+VALU phase issues first.  s_setprio ends
         // a scheduling region: each phase carries its own interleave.
         __builtin_amdgcn_s_setprio(1);
-        qk_tile<D, NW>(kbuf + ((t + 1) & 1) * T::TILE, qf, sn, lane);
+        if constexpr (!LAST) qk_tile<D, NW>(kbuf + ((t + 1) & 1) * T::TILE, qf, sn, lane);
         f16x8 pf[T::PC];
         float ps[4] = {0.f, 0.f, 0.f, 0.f};
         if (act) {
             if constexpr (D == 64) exp_part<D, NW, 0, T::PC / 2>(sc, pf, ms_run, ps, sl2);
             else exp_part<D, NW, 0, T::PC>(sc, pf, ms_run, ps, sl2);
-            __builtin_amdgcn_sched_group_barrier(0x100, kKPrefetch, 0);
+            if constexpr (!LAST) {
+                __builtin_amdgcn_sched_group_barrier(0x100, kKPrefetch, 0);
 #pragma unroll
-            for (int i = 0; i < T::KB * T::DC; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (S of the next tile)
-                __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);  // VALU (this tile's P)
-                __builtin_amdgcn_sched_group_barrier(0x400, kExpPerMfma, 0);  // exp
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // next K fragment read
+                for (int i = 0; i < T::KB * T::DC; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (S of the next tile)
+                    __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);  // VALU (this tile's P)
+                    __builtin_amdgcn_sched_group_barrier(0x400, kExpPerMfma, 0);  // exp
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // next K fragment read
+                }
             }
-        } else {
+        } else if constexpr (!LAST) {
             __builtin_amdgcn_sched_group_barrier(0x100, kKPrefetch, 0);
         }
         __builtin_amdgcn_s_setprio(0);
@@ -469,22 +471,27 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
         }
         __builtin_amdgcn_s_setprio(0);
     };
+    // Tiles 0 .. nkt-2 compute the next tile's S; the last tile's body has no
+    // QK^T (nkt >= 1: every query tile has a key).
+    const int um = min(kt_mask, nkt - 1);
     int t = 0;
-    for (; t + 1 < kt_mask; t += 2) {
-        body(t, sx, sy, std::false_type{});
-        body(t + 1, sy, sx, std::false_type{});
+    for (; t + 1 < um; t += 2) {
+        body(t, sx, sy, std::false_type{}, std::false_type{});
+        body(t + 1, sy, sx, std::false_type{}, std::false_type{});
     }
-    if (t < kt_mask) {
-        body(t, sx, sy, std::false_type{});
+    if (t < um) {
+        body(t, sx, sy, std::false_type{}, std::false_type{});
 #pragma unroll
         for (int b = 0; b < T::KB; ++b) sx[b] = sy[b];
         ++t;
     }
-    for (; t < nkt; ++t) {
-        body(t, sx, sy, std::true_type{});
+    for (; t < nkt - 1; ++t) {
+        body(t, sx, sy, std::true_type{}, std::false_type{});
 #pragma unroll
         for (int b = 0; b < T::KB; ++b) sx[b] = sy[b];
     }
+    if (t < kt_mask) body(t, sx, sy, std::false_type{}, std::true_type{});
+    else body(t, sx, sy, std::true_type{}, std::true_type{});
 
     // O = O^T / l.  Lane holds query qrow, head dims 32t + 16hh + 8*half + i.
     const float l_tot = pair_sum(l_run);
