@@ -106,25 +106,33 @@ def _sm_count(device_index):
 # unit.  The reference's rule aims at 4 blocks per SM (attnkernels/__init__.py:
 # 94-98, tuned on a T4).  The partition is chosen from max_context_len alone
 # (reading the lengths would cost a host sync), so the rule must hold for
-# uniform and for mixed-length batches.  In the MI355X split-K ablation of
+# uniform and for mixed-length batches.  The MI355X split-K ablation of
 # ``attnkernels.benchsuite`` (every power-of-two partition; 5 uniform and 3
-# mixed-length batches, Hkv=8) a target of 16 per CU reaches >= 92% of the best
-# partition in every case; 4 drops to 75% and 2 to 66% on mixed lengths, where
-# too few splits leave the longest sequences as a tail (results/mi355x.md).
+# mixed-length batches, Hkv=8, results/mi355x.md) sets both constants:
+#   * 16 workgroups per CU: with fewer, the longest sequences of a mixed batch
+#     are left as a tail (the reference's 4 reaches only 78% of the best
+#     partition there);
+#   * at least 2 chunks (512 tokens) per split: a 256-token split pays a
+#     workgroup's fixed costs (page ids, then K/V, before any work; the merge)
+#     for little work.
+# Together they reach >= 90% of the best partition in every case (mean 97%);
+# with 1-chunk splits the worst case is 85%.
 DECODE_WG_PER_CU = 16
+DECODE_MIN_CHUNKS = 2
 REFERENCE_WG_PER_SM = 4
 
 
-def decode_partition(batch, num_kv_heads, max_context_len, device=None, wg_per_cu=DECODE_WG_PER_CU):
+def decode_partition(batch, num_kv_heads, max_context_len, device=None, wg_per_cu=DECODE_WG_PER_CU,
+                     min_chunks=DECODE_MIN_CHUNKS):
     """Tokens per split for paged_decode: enough splits for about ``wg_per_cu``
-    workgroups per CU in total, at least one 256-token chunk per split
-    (reference attnkernels/__init__.py:93-101, whose rule is
-    ``wg_per_cu=REFERENCE_WG_PER_SM``)."""
+    workgroups per CU in total, at least ``min_chunks`` 256-token chunks per
+    split where the context has them (reference attnkernels/__init__.py:93-101,
+    whose rule is ``wg_per_cu=REFERENCE_WG_PER_SM, min_chunks=1``)."""
     dev = torch.cuda.current_device() if device is None else device
     blocks = batch * num_kv_heads
     want = -(-int(wg_per_cu) * _sm_count(dev) // blocks)
     max_chunks = -(-max_context_len // CHUNK)
-    splits = max(1, min(want, max_chunks))
+    splits = max(1, min(want, -(-max_chunks // int(min_chunks))))
     return -(-max_chunks // splits) * CHUNK
 
 

@@ -50,35 +50,50 @@ def test_decode_partition_matches_reference_t4_run(monkeypatch):
     monkeypatch.setattr(ak, "_sm_count", lambda dev: fx["sm_count"])
     for r in fx["rows"]:
         assert ak.decode_partition(r["batch"], r["num_kv_heads"], r["max_context_len"], 0,
-                                   wg_per_cu=ak.REFERENCE_WG_PER_SM) == r["partition"], r
+                                   wg_per_cu=ak.REFERENCE_WG_PER_SM, min_chunks=1) == r["partition"], r
 
 
 def test_decode_partition_on_256_cus(monkeypatch):
     monkeypatch.setattr(ak, "_sm_count", lambda dev: 256)
-    for b, hkv, ctx in [(64, 32, 4096), (8, 32, 32768), (1, 8, 32768), (3, 8, 1)]:
-        assert ak.decode_partition(b, hkv, ctx, 0) == \
+    for b, hkv, ctx in [(64, 32, 4096), (8, 32, 32768), (1, 8, 32768), (3, 8, 1), (64, 8, 1024)]:
+        assert ak.decode_partition(b, hkv, ctx, 0, min_chunks=1) == \
             oracle.decode_partition(b, hkv, ctx, 256, wg_per_sm=ak.DECODE_WG_PER_CU)
-        assert ak.decode_partition(b, hkv, ctx, 0, wg_per_cu=4) == oracle.decode_partition(b, hkv, ctx, 256)
+        assert ak.decode_partition(b, hkv, ctx, 0, wg_per_cu=4, min_chunks=1) == oracle.decode_partition(b, hkv, ctx, 256)
+    # The default floor of 2 chunks per split, where the reference's rule gives 256 tokens:
+    # 512 splits wanted but 64 at most (128 chunks); 8 wanted, 2 at most (4 chunks);
+    # a 1-token context keeps one 256-token split.
+    assert ak.DECODE_MIN_CHUNKS == 2
+    assert oracle.decode_partition(1, 8, 32768, 256, wg_per_sm=16) == 256
+    assert ak.decode_partition(1, 8, 32768, 0) == 512
+    assert oracle.decode_partition(64, 8, 1024, 256, wg_per_sm=16) == 256
+    assert ak.decode_partition(64, 8, 1024, 0) == 512
+    assert ak.decode_partition(3, 8, 1, 0) == 256
+    assert ak.decode_partition(3, 8, 300, 0) == 512   # 2 chunks: one split
+    assert ak.decode_partition(64, 32, 4096, 0) == 2048   # the floor does not bind
 
 
 def test_decode_partition_default_is_near_the_measured_optimum(monkeypatch):
     """On 256 CUs the default rule picks a partition within 12% of the fastest
     one in every case of the MI355X split-K ablation, uniform and mixed context
     lengths (tests/golden/decode_partition_mi355x.json: bandwidth of every
-    power-of-two partition per case); the reference's factor does not."""
+    power-of-two partition per case); the reference's rule does not, nor does
+    the default factor without the 2-chunk floor."""
     fx = json.loads((GOLDEN / "decode_partition_mi355x.json").read_text())
     monkeypatch.setattr(ak, "_sm_count", lambda dev: fx["cu_count"])
     assert fx["rows"] and any(r["mixed_lengths"] for r in fx["rows"])
 
-    def worst(factor):
+    def worst(factor, min_chunks):
         fr = []
         for r in fx["rows"]:
-            p = ak.decode_partition(r["batch"], r["num_kv_heads"], r["max_context_len"], 0, wg_per_cu=factor)
+            p = ak.decode_partition(r["batch"], r["num_kv_heads"], r["max_context_len"], 0, wg_per_cu=factor,
+                                    min_chunks=min_chunks)
             fr.append(r["gbs"][str(p)] / max(r["gbs"].values()))
         return min(fr)
 
-    assert worst(ak.DECODE_WG_PER_CU) >= 0.88
-    assert worst(ak.REFERENCE_WG_PER_SM) < worst(ak.DECODE_WG_PER_CU)
+    best = worst(ak.DECODE_WG_PER_CU, ak.DECODE_MIN_CHUNKS)
+    assert best >= 0.88
+    assert worst(ak.REFERENCE_WG_PER_SM, 1) < best
+    assert worst(ak.DECODE_WG_PER_CU, 1) < best
 
 
 def test_reference_module_attention_matches_oracle():
