@@ -1,11 +1,13 @@
 """Benchmark of the attention hot path on one MI355X; prints ONE JSON line.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S] [--settle-seconds T]
 
 Headline (``value``): causal flash prefill, B=2, H=32, N=8192, D=128 fp16
 (where the north-star target is stated), in TFLOP/s with
 the reference's FLOP convention 4*B*H*N^2*D/2 (bench/bench.py:153).  A step is
-one prefill call over that batch with inputs already resident in HBM.
+one prefill call over that batch with inputs already resident in HBM.  Each
+workload first runs untimed for --settle-seconds (the GPU's clock leaves its
+idle state), then W untimed warmup steps, then the K timed steps.
 
 The same line carries, under ``workloads``, the other BASELINE configs measured
 the same way: non-causal prefill, the N=8191 variant, the two
@@ -77,14 +79,28 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+# Seconds of untimed calls before each workload's W warmup steps (--settle-seconds).
+# On MI355X a kernel stream started from idle runs about 6% slower for its first
+# ~50 ms (causal prefill, same box: 990 TFLOP/s after 5 warmup steps, 1051 after
+# 50, 1056 in a long-running loop), so a few steps of warmup measure the ramp,
+# not the steady state a serving or training loop runs in.
+SETTLE_S = 0.25
+
+
 def timed_steps(fn, steps, warmup):
-    """W untimed calls, then exactly K calls bracketed by synchronize, with one
-    HIP event on the current (launch) stream at each step boundary (K+1
-    events): step i lasts from event i to event i+1.  One marker per step, not
-    a start and an end, keeps the events' own cost out of short kernels' times.
+    """Untimed calls for SETTLE_S seconds, then W untimed calls, then exactly K
+    calls bracketed by synchronize, with one HIP event on the current (launch)
+    stream at each step boundary (K+1 events): step i lasts from event i to
+    event i+1.  One marker per step, not a start and an end, keeps the events'
+    own cost out of short kernels' times.
     Returns (total_ms, mean_event_ms, median_event_ms)."""
     import torch
 
+    settle_end = time.perf_counter() + SETTLE_S
+    while time.perf_counter() < settle_end:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -328,11 +344,14 @@ def cpu_configs():
 
 
 def main():
+    global SETTLE_S
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--settle-seconds", type=float, default=SETTLE_S,
+                    help="untimed calls of each workload before its warmup steps (clock settle)")
     ap.add_argument("--only", default="all",
                     help="all | headline | prefill | decode | comma list of workload names")
     ap.add_argument("--calib-copy", action="store_true",
@@ -360,6 +379,7 @@ def main():
         del src, dst
         torch.cuda.empty_cache()
     K, W = args.steps, args.warmup
+    SETTLE_S = max(0.0, args.settle_seconds)
     lens4 = torch.randint(1, 4097, (64,), generator=torch.Generator().manual_seed(4)).tolist()
     lensv = torch.randint(512, 8193, (16,), generator=torch.Generator().manual_seed(5)).tolist()
     cases = {  # BASELINE.json configs[1..4]
@@ -405,7 +425,7 @@ def main():
     ach = headline["kernel_tflops"]
     line = {
         "metric": "prefill TFLOP/s (% MFMA peak); paged decode KV GB/s (% HBM peak)",
-        "value": headline["value"], "unit": "TFLOP/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "value": headline["value"], "unit": "TFLOP/s", "n_gpus": 1, "steps": K, "warmup": W, "settle_s": SETTLE_S,
         "ms_per_step": headline["ms_per_step"], "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
         "config": {"workload": headline["workload"] + " (BASELINE configs[2])", "global_batch": 2,
