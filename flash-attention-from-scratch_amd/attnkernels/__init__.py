@@ -115,7 +115,7 @@ def _sm_count(device_index):
 #   * at least 2 chunks (512 tokens) per split: a 256-token split pays a
 #     workgroup's fixed costs (page ids, then K/V, before any work; the merge)
 #     for little work.
-# Together they reach >= 90% of the best partition in every case (mean 97%);
+# Together they reach >= 88% of the best partition in every case (mean 96%);
 # with 1-chunk splits the worst case is 85%.
 DECODE_WG_PER_CU = 16
 DECODE_MIN_CHUNKS = 2
