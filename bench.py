@@ -12,8 +12,9 @@ idle state), then W untimed warmup steps, then the K timed steps.
 The same line carries, under ``workloads``, the other BASELINE configs measured
 the same way: non-causal prefill, the N=8191 variant, the two
 paged split-K decode configs in KV GB/s with the reference's byte convention
-sum(ctx)*Hkv*D*2*2 (bench/bench.py:199-200), and the paged cache writer
-(K/V rows read + written, GB/s), and a packed variable-length GQA prefill.
+sum(ctx)*Hkv*D*2*2 (bench/bench.py:199-200), a grouped-query decode layer (4
+query heads per kv head) at the library's default partition, the paged cache
+writer (K/V rows read + written, GB/s), and a packed variable-length GQA prefill.
 
 ``roofline`` is the headline kernel's algorithmic FLOP per launch divided by its
 mean launch duration (HIP events on the launch stream, inside the timed
@@ -151,6 +152,8 @@ def decode_case(lens, hkv, d, bs, partition, steps, warmup, seed=0, hq=None):
     import attnkernels as ak
 
     hq = hkv if hq is None else hq
+    if partition is None:  # the library's default split rule
+        partition = ak.decode_partition(len(lens), hkv, max(lens))
     nblk = [-(-c // bs) for c in lens]
     pool = -(-sum(nblk) * 11 // 10)
     rng = np.random.default_rng(seed)
@@ -389,6 +392,8 @@ def main():
         "decode_ragged64_d128": lambda: decode_case(lens4, 32, 128, 16, 512, K, W),
         "decode_long8_d128": lambda: decode_case([32768] * 8, 32, 128, 16, 256, K, W),
         "decode_long8_d64": lambda: decode_case([32768] * 8, 32, 64, 16, 256, K, W),
+        # a Llama-3-8B-like decode layer: 4 query heads per kv head, the default partition
+        "decode_gqa16_d128": lambda: decode_case([8192] * 16, 8, 128, 16, None, K, W, hq=32),
         # packed prompts of mixed lengths, 4 query heads per kv head, no padding
         "prefill_varlen_gqa": lambda: varlen_case(lensv, 32, 8, 128, True, K, W),
         # the step before decode reads the cache: append a batch of prompts' K/V to it
