@@ -13,10 +13,10 @@
 //   * a token row of one page is D*2 contiguous bytes; D/8 lanes cover it with
 //     one 16-byte load each, so one wave-wide load reads 4 (D=128) or 8 (D=64)
 //     tokens = 1 KB; a D=128 lane keeps 16 K loads and 16 V loads in flight (4
-//     waves per workgroup; 4 and 4 with 4 query heads per kv head, 8 and 8
-//     with 8), a D=64 lane 4 and 4 (8 waves with one query head per kv head,
-//     4 with head groups): the fastest shape of each head size on ragged and
-//     long-context paged caches, as measured on MI355X;
+//     waves per workgroup; with head groups 8 and 8, or 4 and 4 with 4 query
+//     heads per kv head), a D=64 lane 4 and 4 (8 waves with one query head per
+//     kv head, 4 with head groups): the fastest shape of each head size on
+//     ragged and long-context paged caches, as measured on MI355X;
 //   * the dot product is v_dot2_f32_f16 on the raw fp16 q and k, reduced over
 //     the D/8 lanes of a token with DPP row permutes, then scaled by
 //     scale*log2(e) in fp32;
@@ -47,9 +47,10 @@ struct DecodeTile {
     static constexpr int LPT = D / 8;            // lanes per token row
     static constexpr int TPL = kWave / LPT;      // tokens per wave-wide load
     // Loads in flight per lane, per cache.  D=128 with head groups spends the
-    // registers on q and the accumulators instead: 8 with 8 query heads per kv
-    // head; 4 with 4, where 115 VGPRs leave 4 waves per SIMD rather than 3.
-    static constexpr int U = D == 128 ? (G <= 2 ? 16 : G == 4 ? 4 : 8) : 4;
+    // registers on q and the accumulators instead, for more waves per SIMD: 8
+    // with 2 query heads per kv head (127 VGPRs, 4 waves, against 229 and 2 at
+    // 16) and with 8; 4 with 4 (115 VGPRs, 4 waves, against 162 and 3 at 8).
+    static constexpr int U = D == 128 ? (G == 1 ? 16 : G == 4 ? 4 : 8) : 4;
     static constexpr int TOK = U * TPL;         // tokens per wave iteration
     // Page size of the fast path: a wave iteration then covers PPI whole pages
     // (its first token is a multiple of TOK, itself a multiple of 16).
