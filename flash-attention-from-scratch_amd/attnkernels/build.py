@@ -13,6 +13,7 @@ Two artefacts, both next to this file:
 """
 from __future__ import annotations
 
+import hashlib
 import os
 import shutil
 import subprocess
@@ -109,13 +110,34 @@ def build_extension(verbose=False):
 
 def build(verbose=False):
     """Build both artefacts; always recompiles."""
+    digest = sources_digest()
     build_library(verbose)
     build_extension(verbose)
+    STAMP.write_text(digest + "\n")
     return LIB, ext_path()
 
 
+STAMP = OBJ / "sources.sha256"
+
+
+def sources_digest() -> str:
+    """SHA-256 over the names and contents of every source and header the two
+    artefacts are built from (this file included: it holds the flags)."""
+    h = hashlib.sha256()
+    files = sorted(p for d in (CSRC, INCLUDE) for p in d.iterdir() if p.suffix in (".hip", ".cpp", ".hpp", ".h"))
+    for p in files + [Path(__file__).resolve()]:
+        h.update(p.name.encode())
+        h.update(p.read_bytes())
+    return h.hexdigest()
+
+
 def is_built() -> bool:
-    return LIB.exists() and ext_path().exists()
+    """Both artefacts exist and were built from the sources as they are now
+    (a digest written at build time; file times may not survive a copy of the
+    tree).  A stale library would run old kernels under current tests."""
+    if not (LIB.exists() and ext_path().exists() and STAMP.exists()):
+        return False
+    return STAMP.read_text().strip() == sources_digest()
 
 
 if __name__ == "__main__":

@@ -269,14 +269,19 @@ paged_decode_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const
         float M = -INFINITY;
 #pragma unroll
         for (int v = 0; v < T::NW; ++v) M = fmaxf(M, red_m[v][h]);
+        // A split whose every token sits on an out-of-range page has no valid
+        // token in any wave: M stays -inf, and subtracting it would give
+        // 2^(-inf + inf) = NaN.  Such a split yields o = 0, l = 0, m = -inf,
+        // which the reduce weighs 0.
+        const float Mu = M == -INFINITY ? 0.f : M;
         float L = 0.f, o = 0.f;
 #pragma unroll
         for (int v = 0; v < T::NW; ++v) {
-            const float wv = exp2_fast(red_m[v][h] - M);  // waves without tokens: 2^-inf = 0
+            const float wv = exp2_fast(red_m[v][h] - Mu);  // waves without tokens: 2^-inf = 0
             L += red_l[v][h] * wv;
             o += red_acc[v][h][d] * wv;
         }
-        o /= L;
+        o = L > 0.f ? o / L : 0.f;
         const size_t row = (size_t)b * hq + kvh * G + h;
         if (num_splits == 1) {
             out[row * D + d] = (f16)o;
@@ -292,7 +297,11 @@ paged_decode_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const
 
 // LSE merge of the split partials (paged_decode.cu:204-215): one 256-thread
 // workgroup per (sequence, query head) row; ns = ceil(ctx/P) partials are
-// merged, clamped to the number of launched splits.  Every partial is read by
+// merged, with ctx clamped to the table row's capacity max_tok exactly as the
+// decode kernel clamps it (a split starting past max_tok writes no partial),
+// and ns clamped to the number of launched splits.  Partials with l = 0 (no
+// readable token in the split) carry no weight; a row with no weight at all
+// is written as zeros.  Every partial is read by
 // an independent load (no serial chain over splits): pass 1 takes the block
 // max of m; pass 2 has D/4 threads per partial row, each with a float4 of o,
 // and 256/(D/4) partial rows in flight per step; the groups are summed in LDS.
@@ -300,14 +309,14 @@ template <int D>
 __global__ void __launch_bounds__(256)
 paged_reduce_kernel(const float* __restrict__ o_part, const float* __restrict__ m_part,
                     const float* __restrict__ l_part, const int* __restrict__ ctx_lens,
-                    f16* __restrict__ out, int hq, int partition, int num_splits) {
+                    f16* __restrict__ out, int hq, int partition, int num_splits, int max_tok) {
     constexpr int THREADS = 256, TPR = D / 4, GROUPS = THREADS / TPR;
     __shared__ float red_max[THREADS / kWave];
     __shared__ f32x4 red_acc[GROUPS][TPR];
     __shared__ float red_den[GROUPS];
     const size_t row = blockIdx.x;
     const int b = (int)(row / hq);
-    const int ctx = ctx_lens[b];
+    const int ctx = min(ctx_lens[b], max_tok);
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     int ns = ctx > 0 ? (int)(((long long)ctx + partition - 1) / partition) : 0;
     ns = min(ns, num_splits);
@@ -322,13 +331,15 @@ paged_reduce_kernel(const float* __restrict__ o_part, const float* __restrict__ 
     if (lane == 0) red_max[w] = M;
     __syncthreads();
     M = fmaxf(fmaxf(red_max[0], red_max[1]), fmaxf(red_max[2], red_max[3]));
+    if (M == -INFINITY) M = 0.f;  // every partial empty: all weights are 0 below
 
     const int g = tid / TPR, j = tid % TPR;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     float den = 0.f;
 #pragma unroll 4
     for (int s = g; s < ns; s += GROUPS) {
-        const float wgt = lp[s] * exp2_fast(mp[s] - M);
+        const float ls = lp[s];
+        const float wgt = ls > 0.f ? ls * exp2_fast(mp[s] - M) : 0.f;
         acc += wgt * op[(size_t)s * TPR + j];
         den += wgt;
     }
@@ -343,7 +354,7 @@ paged_reduce_kernel(const float* __restrict__ o_part, const float* __restrict__ 
             sum += red_acc[k][tid];
             dsum += red_den[k];
         }
-        const float inv = ns > 0 ? 1.f / dsum : 0.f;
+        const float inv = dsum > 0.f ? 1.f / dsum : 0.f;
         f16* dst = out + row * D + tid * 4;
 #pragma unroll
         for (int i = 0; i < 4; ++i) dst[i] = (f16)(sum[i] * inv);
@@ -366,7 +377,7 @@ static hipError_t launch_decode(const DecodeArgs& a) {
     if (e != hipSuccess || a.num_splits == 1) return e;
     hipLaunchKernelGGL((paged_reduce_kernel<D>), dim3((unsigned)(a.batch * a.hq)), dim3(256), 0, stream,
                        a.o_part, a.m_part, a.l_part, a.context_lens, (f16*)a.out, (int)a.hq,
-                       (int)a.partition, (int)a.num_splits);
+                       (int)a.partition, (int)a.num_splits, (int)(a.max_blocks * a.bs));
     return hipGetLastError();
 }
 

@@ -68,3 +68,26 @@ def test_capi_paged_decode_with_workspace(lib):
     assert lib.ak_paged_decode(*args, ptr(ws), need, stream()) == 0, lib.ak_last_error()
     torch.cuda.synchronize()
     assert max_err(out, oracle.paged_decode_fp32(q, kc, vc, bt, cl)) < TOL[128]
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 4), (4, 4)])
+def test_capi_context_beyond_table_capacity(lib, hq, hkv):
+    """context_lens larger than the table row (32 pages x 16 = 512 tokens) with
+    max_context_len 1000 and 256-token splits: splits 2 and 3 start past the
+    table and write no partial; the reduce must not read them.  The workspace
+    is pre-filled with NaN, so reading one would show."""
+    lens = [512, 300]
+    kc, vc, bt, _ = oracle.make_paged_cache(lens, hkv, 128, block_size=16, extra_blocks=3, seed=12)
+    cl = np.asarray([1000, 300], np.int32)
+    q = np.random.default_rng(13).standard_normal((2, hq, 128), dtype=np.float32).astype(np.float16)
+    qd, kcd, vcd, btd, cld = (torch.from_numpy(a).cuda() for a in (q, kc, vc, bt, cl))
+    out = torch.empty_like(qd)
+    need = lib.ak_paged_decode_workspace_size(2, hq, 128, 1000, 256)
+    ws = torch.full((need // 4,), float("nan"), dtype=torch.float32, device="cuda")
+    rc = lib.ak_paged_decode(ptr(qd), ptr(kcd), ptr(vcd), ptr(btd), ptr(cld), ptr(out), 2, hq, hkv, 128,
+                             kc.shape[0], 16, bt.shape[1], 1000, 128 ** -0.5, 256, ptr(ws), need, stream())
+    assert rc == 0, lib.ak_last_error()
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    ref = oracle.paged_decode_fp32(q, kc, vc, bt, np.asarray([512, 300], np.int32))
+    assert max_err(out, ref) < TOL[128]

@@ -62,7 +62,8 @@ def test_ragged_batch(d, partition):
 CHUNK_EDGES = [15, 16, 17, 31, 32, 33, 63, 65, 127, 129, 255, 257, 383, 385, 511, 513]
 
 
-@pytest.mark.parametrize("d,hq,hkv", [(128, 16, 4), (128, 64, 8), (64, 8, 4), (64, 32, 4), (64, 64, 8)])
+@pytest.mark.parametrize("d,hq,hkv", [(128, 16, 4), (128, 64, 8), (128, 8, 4), (64, 8, 4), (64, 32, 4),
+                                      (64, 64, 8)])
 @pytest.mark.parametrize("partition", [256, 512])
 def test_chunk_edges_head_groups(d, hq, hkv, partition):
     """Context lengths one token either side of every chunk size the head-group
@@ -122,7 +123,8 @@ def test_errors_match_reference():
 
 # ------------------------------------------------ bit-exact page gathering --
 
-@pytest.mark.parametrize("d,bs,group", [(128, 16, 1), (64, 8, 1), (128, 32, 1), (128, 16, 4), (64, 16, 8)])
+@pytest.mark.parametrize("d,bs,group", [(128, 16, 1), (64, 8, 1), (128, 32, 1), (128, 16, 4), (128, 16, 2),
+                                        (64, 16, 8)])
 def test_gather_reads_exact_token(d, bs, group):
     """Each (sequence, kv head) attends to one chosen token only (its key gets a
     +64 score, every other key -64, scale 1): the output must be that token's V
@@ -189,6 +191,42 @@ def test_bad_page_ids_are_not_read(d, hq, hkv, ctx, bad, bad_id):
     g = hq // hkv
     ref = np.stack([oracle.attention_fp32(q[0, h][None], kk[h // g], vv[h // g])[0] for h in range(hq)])
     assert max_err(out[0], ref) < TOL[d]
+
+
+def _ref_without_pages(q, kc, vc, bt, ctx, bad_pages, hq, hkv):
+    """Oracle for one sequence whose tokens on ``bad_pages`` (table slots) are
+    left out; a zero row when no token is left."""
+    d = q.shape[-1]
+    keep = np.array([t for t in range(ctx) if t // 16 not in bad_pages], dtype=np.int64)
+    if keep.size == 0:
+        return np.zeros((hq, d), np.float32)
+    nblk = -(-ctx // 16)
+    kk = oracle.gather_kv(kc, bt, nblk)[0][:, keep]
+    vv = oracle.gather_kv(vc, bt, nblk)[0][:, keep]
+    g = hq // hkv
+    return np.stack([oracle.attention_fp32(q[h][None], kk[h // g], vv[h // g])[0] for h in range(hq)])
+
+
+@pytest.mark.parametrize("d,hq,hkv", [(128, 8, 8), (128, 16, 4), (64, 8, 8), (64, 16, 2)])
+@pytest.mark.parametrize("partition", [256, 1 << 20])
+def test_bad_pages_cover_a_whole_split_or_sequence(d, hq, hkv, partition):
+    """Every token of one 256-token split sits on out-of-range page ids
+    (sequence 0, tokens 256..511), and every token of sequence 1: those tokens
+    drop out of the softmax, the split with none left carries no weight in the
+    merge, and the sequence with none left gets a zero row (no NaN)."""
+    lens = [1000, 700, 300]
+    kc, vc, bt, cl = cache(lens, hkv, d, extra=0, seed=43)
+    bt_bad = bt.copy()
+    bad0 = set(range(16, 32))
+    bt_bad[0, sorted(bad0)] = 10 ** 6
+    bt_bad[1, :] = -1
+    q = rand_q(len(lens), hq, d, seed=44)
+    out = ak.paged_decode(*to_dev(q, kc, vc, bt_bad, cl), max(lens), partition_size=partition)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    assert max_err(out[0], _ref_without_pages(q[0], kc, vc, bt[0:1], lens[0], bad0, hq, hkv)) < TOL[d]
+    assert torch.count_nonzero(out[1]) == 0
+    assert max_err(out[2:3], oracle.paged_decode_fp32(q[2:3], kc, vc, bt[2:3], cl[2:3])) < TOL[d]
 
 
 # ---------------------------------------------------- BASELINE full sizes --
