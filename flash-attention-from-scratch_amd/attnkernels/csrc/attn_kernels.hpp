@@ -55,6 +55,12 @@ struct CacheWriteArgs {
 
 hipError_t prefill_launch(const PrefillArgs& a);
 hipError_t decode_launch(const DecodeArgs& a);
+
+// Size of the static per-GPU split-partials array behind
+// ak_paged_decode_noalloc, and its device address on the current GPU
+// (looked up once per device).
+constexpr size_t kDecodeScratchBytes = size_t(32) << 20;
+hipError_t decode_scratch(void** ptr);
 hipError_t cache_write_launch(const CacheWriteArgs& a);
 
 }  // namespace ak

@@ -9,6 +9,9 @@
 #include "attn_kernels.hpp"
 #include "attnkernels.h"
 
+static_assert(AK_PAGED_DECODE_NOALLOC_MAX_BYTES == ak::kDecodeScratchBytes,
+              "the header states the static scratch size");
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -70,6 +73,68 @@ int prefill(const char* who, const void* q, const void* k, const void* v, void* 
     a.qflip = std::signbit(scale) && scale != 0.0 ? 0x80008000u : 0u;
     a.stream = stream;
     return hip_status(ak::prefill_launch(a), who);
+}
+
+// Validation shared by both decode entry points, in the reference's order
+// (paged_decode.cu:260-262, 275), and the launch arguments except the split
+// partials.  batch == 0 passes validation with nothing to launch.
+int decode_args(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_tables,
+                const int32_t* context_lens, void* out, int64_t batch, int64_t num_heads, int64_t num_kv_heads,
+                int64_t head_dim, int64_t num_blocks, int64_t block_size, int64_t max_blocks_per_seq,
+                int64_t max_context_len, double scale, int64_t partition, void* stream, ak::DecodeArgs& a) {
+    if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0)
+        return fail(AK_ERR_INVALID_ARGUMENT, "num_heads must be a multiple of num_kv_heads");
+    if (partition <= 0 || partition % kChunk != 0)
+        return fail(AK_ERR_INVALID_ARGUMENT, "partition size must be a positive multiple of 256");
+    const int64_t G = num_heads / num_kv_heads;
+    if ((head_dim != 64 && head_dim != 128) || (G != 1 && G != 2 && G != 4 && G != 8))
+        return fail(AK_ERR_UNSUPPORTED,
+                    "paged_decode: head_dim must be 64/128 and num_heads/num_kv_heads in {1,2,4,8}");
+    if (batch < 0 || num_blocks < 0 || block_size <= 0 || max_blocks_per_seq < 0)
+        return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: invalid size");
+    if (batch == 0) return ok();
+    if (max_context_len < 1)
+        return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: max_context_len must be >= 1");
+    if (max_blocks_per_seq < 1 || num_blocks < 1)
+        return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: empty block table or cache");
+    if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !out)
+        return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: null pointer");
+    if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
+        return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: q, caches and out must be 16-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(block_tables) & 3u) || (reinterpret_cast<uintptr_t>(context_lens) & 3u))
+        return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: int32 arrays must be 4-byte aligned");
+    if (max_context_len > INT_MAX - partition || partition > INT_MAX || num_blocks > INT_MAX ||
+        max_blocks_per_seq * block_size > INT_MAX || batch > 65535 || num_kv_heads > 65535)
+        return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: size out of range");
+    const int64_t splits = (max_context_len + partition - 1) / partition;
+    if (splits > 65535) return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: more than 65535 splits");
+    a.q = q;
+    a.k_cache = k_cache;
+    a.v_cache = v_cache;
+    a.block_tables = block_tables;
+    a.context_lens = context_lens;
+    a.out = out;
+    a.batch = batch;
+    a.hq = num_heads;
+    a.hkv = num_kv_heads;
+    a.d = head_dim;
+    a.num_blocks = num_blocks;
+    a.bs = block_size;
+    a.max_blocks = max_blocks_per_seq;
+    a.partition = partition;
+    a.num_splits = splits;
+    a.sl2 = (float)(scale * kLog2e);
+    a.stream = stream;
+    return ok();
+}
+
+// Split partials laid out in one fp32 buffer: o [B, Hq, S, D], m [B, Hq, S], l [B, Hq, S].
+void set_partials(ak::DecodeArgs& a, void* buf) {
+    float* ws = static_cast<float*>(buf);
+    const size_t rows = (size_t)a.batch * (size_t)a.hq * (size_t)a.num_splits;
+    a.o_part = ws;
+    a.m_part = ws + rows * (size_t)a.d;
+    a.l_part = a.m_part + rows;
 }
 
 }  // namespace
@@ -139,65 +204,57 @@ int ak_paged_decode(const void* q, const void* k_cache, const void* v_cache, con
                     int64_t num_kv_heads, int64_t head_dim, int64_t num_blocks, int64_t block_size,
                     int64_t max_blocks_per_seq, int64_t max_context_len, double scale, int64_t partition,
                     void* workspace, size_t workspace_bytes, void* stream) {
-    // Checks in the reference's order (paged_decode.cu:260-262, 275).
-    if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0)
-        return fail(AK_ERR_INVALID_ARGUMENT, "num_heads must be a multiple of num_kv_heads");
-    if (partition <= 0 || partition % kChunk != 0)
-        return fail(AK_ERR_INVALID_ARGUMENT, "partition size must be a positive multiple of 256");
-    const int64_t G = num_heads / num_kv_heads;
-    if ((head_dim != 64 && head_dim != 128) || (G != 1 && G != 2 && G != 4 && G != 8))
-        return fail(AK_ERR_UNSUPPORTED,
-                    "paged_decode: head_dim must be 64/128 and num_heads/num_kv_heads in {1,2,4,8}");
-    if (batch < 0 || num_blocks < 0 || block_size <= 0 || max_blocks_per_seq < 0)
-        return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: invalid size");
-    if (batch == 0) return ok();
-    if (max_context_len < 1)
-        return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: max_context_len must be >= 1");
-    if (max_blocks_per_seq < 1 || num_blocks < 1)
-        return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: empty block table or cache");
-    if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !out)
-        return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: null pointer");
-    if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
-        return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: q, caches and out must be 16-byte aligned");
-    if ((reinterpret_cast<uintptr_t>(block_tables) & 3u) || (reinterpret_cast<uintptr_t>(context_lens) & 3u))
-        return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: int32 arrays must be 4-byte aligned");
-    if (max_context_len > INT_MAX - partition || partition > INT_MAX || num_blocks > INT_MAX ||
-        max_blocks_per_seq * block_size > INT_MAX || batch > 65535 || num_kv_heads > 65535)
-        return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: size out of range");
-    const int64_t splits = (max_context_len + partition - 1) / partition;
-    if (splits > 65535) return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: more than 65535 splits");
     ak::DecodeArgs a{};
-    if (splits > 1) {
+    const int rc = decode_args(q, k_cache, v_cache, block_tables, context_lens, out, batch, num_heads, num_kv_heads,
+                               head_dim, num_blocks, block_size, max_blocks_per_seq, max_context_len, scale,
+                               partition, stream, a);
+    if (rc != AK_OK || batch == 0) return rc;
+    if (a.num_splits > 1) {
         const size_t need = ak_paged_decode_workspace_size(batch, num_heads, head_dim, max_context_len, partition);
         if (!workspace || workspace_bytes < need)
             return fail(AK_ERR_WORKSPACE, "paged_decode: workspace of " + std::to_string(need) +
                                               " bytes required, got " + std::to_string(workspace_bytes));
         if (!aligned16(workspace))
             return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: workspace must be 16-byte aligned");
-        float* ws = static_cast<float*>(workspace);
-        const size_t rows = (size_t)batch * (size_t)num_heads * (size_t)splits;
-        a.o_part = ws;
-        a.m_part = ws + rows * (size_t)head_dim;
-        a.l_part = a.m_part + rows;
+        set_partials(a, workspace);
     }
-    a.q = q;
-    a.k_cache = k_cache;
-    a.v_cache = v_cache;
-    a.block_tables = block_tables;
-    a.context_lens = context_lens;
-    a.out = out;
-    a.batch = batch;
-    a.hq = num_heads;
-    a.hkv = num_kv_heads;
-    a.d = head_dim;
-    a.num_blocks = num_blocks;
-    a.bs = block_size;
-    a.max_blocks = max_blocks_per_seq;
-    a.partition = partition;
-    a.num_splits = splits;
-    a.sl2 = (float)(scale * kLog2e);
-    a.stream = stream;
     return hip_status(ak::decode_launch(a), "paged_decode");
+}
+
+int ak_paged_decode_noalloc(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_tables,
+                            const int32_t* context_lens, void* out, int64_t batch, int64_t num_heads,
+                            int64_t num_kv_heads, int64_t head_dim, int64_t num_blocks, int64_t block_size,
+                            int64_t max_blocks_per_seq, int64_t max_context_len, double scale, int64_t partition,
+                            void* stream) {
+    ak::DecodeArgs a{};
+    const int rc = decode_args(q, k_cache, v_cache, block_tables, context_lens, out, batch, num_heads, num_kv_heads,
+                               head_dim, num_blocks, block_size, max_blocks_per_seq, max_context_len, scale,
+                               partition, stream, a);
+    if (rc != AK_OK || batch == 0) return rc;
+    if (a.num_splits > 1) {
+        const size_t need = ak_paged_decode_workspace_size(batch, num_heads, head_dim, max_context_len, partition);
+        if (need > ak::kDecodeScratchBytes)
+            return fail(AK_ERR_WORKSPACE, "paged_decode_noalloc: the split partials need " + std::to_string(need) +
+                                              " bytes, more than the static scratch of " +
+                                              std::to_string(ak::kDecodeScratchBytes) +
+                                              " bytes; use a larger partition or ak_paged_decode with a workspace");
+        // The scratch array of the current device: the stream must run there.
+        if (stream) {
+            int cur = 0;
+            hipDevice_t sdev = 0;
+            hipError_t e = hipGetDevice(&cur);
+            if (e == hipSuccess) e = hipStreamGetDevice((hipStream_t)stream, &sdev);
+            if (e != hipSuccess) return hip_status(e, "paged_decode_noalloc");
+            if ((int)sdev != cur)
+                return fail(AK_ERR_INVALID_ARGUMENT,
+                            "paged_decode_noalloc: the stream must belong to the current device");
+        }
+        void* ws = nullptr;
+        const hipError_t e = ak::decode_scratch(&ws);
+        if (e != hipSuccess) return hip_status(e, "paged_decode_noalloc");
+        set_partials(a, ws);
+    }
+    return hip_status(ak::decode_launch(a), "paged_decode_noalloc");
 }
 
 int ak_reshape_and_cache(const void* key, const void* value, void* k_cache, void* v_cache,

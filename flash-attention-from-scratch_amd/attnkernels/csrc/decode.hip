@@ -31,6 +31,7 @@
 #include "attn_kernels.hpp"
 #include "wave.hpp"
 
+#include <mutex>
 #include <type_traits>
 
 namespace ak {
@@ -379,6 +380,37 @@ static hipError_t launch_decode(const DecodeArgs& a) {
                        a.o_part, a.m_part, a.l_part, a.context_lens, (f16*)a.out, (int)a.hq,
                        (int)a.partition, (int)a.num_splits, (int)(a.max_blocks * a.bs));
     return hipGetLastError();
+}
+
+// Split partials of ak_paged_decode_noalloc: one static array per GPU, held
+// until the process ends, so that callers that cannot allocate (graph capture,
+// tight serving loops) need no workspace.  Every call on a GPU shares that
+// GPU's array; calls that overlap on one GPU race.  Nothing in it has to start
+// at zero: the reduce reads only partials the same call's decode kernel wrote.
+static __device__ __align__(256) float scratch[kDecodeScratchBytes / sizeof(float)];
+
+// Device address of this GPU's scratch array.  In host code `scratch` names a
+// host-side stand-in, never the device memory: the address comes from
+// hipGetSymbolAddress, called once per device with that device current, and
+// only that pointer is handed to kernels.
+hipError_t decode_scratch(void** ptr) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static void* addr[kMaxDevices] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        addr[dev] = p;
+    }
+    *ptr = addr[dev];
+    return hipSuccess;
 }
 
 hipError_t decode_launch(const DecodeArgs& a) {

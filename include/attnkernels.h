@@ -116,6 +116,27 @@ int ak_paged_decode(const void *q, const void *k_cache, const void *v_cache,
                     int64_t max_context_len, double scale, int64_t partition, void *workspace,
                     size_t workspace_bytes, void *stream);
 
+/* Paged-KV decode that allocates nothing: ak_paged_decode without the
+ * workspace arguments.  No counterpart in the reference; it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The split partials live in
+ * a static per-GPU device array of AK_PAGED_DECODE_NOALLOC_MAX_BYTES (32 MiB),
+ * held until the process ends; the call fails with AK_ERR_WORKSPACE, before
+ * any HIP call, when ak_paged_decode_workspace_size() for these sizes exceeds
+ * it (e.g. 8 sequences x 32 query heads x 128 splits x D=128 need 17 MB).
+ * The call itself calls no hipMalloc/hipFree; its first call on a device looks
+ * up that device's array (hipGetSymbolAddress).  All calls on one GPU share the
+ * array: calls that overlap on one GPU (other streams, other threads) race.
+ * `stream` must belong to the current device.  Arguments, results and errors
+ * are otherwise those of ak_paged_decode. */
+#define AK_PAGED_DECODE_NOALLOC_MAX_BYTES ((size_t)32 << 20)
+int ak_paged_decode_noalloc(const void *q, const void *k_cache, const void *v_cache,
+                            const int32_t *block_tables, const int32_t *context_lens, void *out,
+                            int64_t batch, int64_t num_heads, int64_t num_kv_heads,
+                            int64_t head_dim, int64_t num_blocks, int64_t block_size,
+                            int64_t max_blocks_per_seq, int64_t max_context_len, double scale,
+                            int64_t partition, void *stream);
+
 /* Paged KV-cache writer ("reshape and cache"): appends new tokens' keys and
  * values to the paged cache that ak_paged_decode reads.  No counterpart in the
  * reference, which only reads the cache (attnkernels/csrc/paged_decode.cu:95-96);

@@ -33,6 +33,7 @@ def lib():
     L.ak_paged_decode_workspace_size.restype = ctypes.c_size_t
     L.ak_paged_decode.argtypes = [vp] * 6 + [i64] * 8 + [f64, i64, vp, ctypes.c_size_t, vp]
     L.ak_reshape_and_cache.argtypes = [vp] * 5 + [i64] * 7 + [vp]
+    L.ak_paged_decode_noalloc.argtypes = [vp] * 6 + [i64] * 8 + [f64, i64, vp]
     L.ak_prefill_gqa.argtypes = [vp] * 4 + [i64] * 5 + [ctypes.c_int, f64, vp]
     L.ak_prefill_varlen.argtypes = [vp] * 5 + [i64] * 6 + [ctypes.c_int, f64, vp]
     return L
@@ -151,3 +152,14 @@ def test_gqa_and_varlen_validation(lib):
     rc = lib.ak_prefill_varlen(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 100, 8, 3, 64, 128, 1, 0.1, None)
     assert rc == 1 and b"multiple of num_kv_heads" in lib.ak_last_error()
     assert lib.ak_prefill_varlen(FAKE, FAKE, FAKE, FAKE, FAKE, 2, 0, 8, 2, 64, 128, 1, 0.1, None) == 0
+
+
+def test_noalloc_decode_rejects_oversized_partials_before_any_hip_call(lib):
+    # 64 x 32 heads x 4096 splits x (128 + 2) floats = 4.4 GB > the 32 MiB static array
+    rc = lib.ak_paged_decode_noalloc(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 64, 32, 8, 128, 100, 16, 65536,
+                                     1 << 20, 0.1, 256, None)
+    assert rc == 3
+    assert b"static scratch" in lib.ak_last_error()
+    # the shared validation still applies first
+    assert lib.ak_paged_decode_noalloc(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1, 6, 4, 128, 100, 16, 8, 100,
+                                       0.1, 256, None) == 1
