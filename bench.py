@@ -18,7 +18,10 @@ writer (K/V rows read + written, GB/s), and a packed variable-length GQA prefill
 
 ``roofline`` is the headline kernel's algorithmic FLOP per launch divided by its
 mean launch duration (HIP events on the launch stream, inside the timed
-region), against the 2.5 PFLOP/s dense fp16 MFMA peak.  ``cpu_baseline`` times
+region), against the 2.5 PFLOP/s dense fp16 MFMA peak.  Every workload is
+also timed a second way, ``flushed``: K more steps, each after 512 MiB of
+device memory is overwritten (outside the step's start/end events), median
+reported, as the reference times every rep after an L2 flush.  ``cpu_baseline`` times
 the numpy oracle (oracle/attention.py) on a bounded sample of the same
 workload on this host's cores.
 """
@@ -88,22 +91,51 @@ def log(msg):
 SETTLE_S = 0.25
 
 
+# Bytes written between flushed steps: twice MI355X's 256 MB Infinity Cache (and
+# far more than the 8 x 4 MB of L2), so a flushed step reads its inputs from HBM.
+# The reference flushes its T4's L2 before every timed rep (bench/bench.py:37-41).
+FLUSH_BYTES = 512 << 20
+_flush_buf = None
+
+
+def flush_caches():
+    """Overwrite FLUSH_BYTES of device memory (one fill kernel)."""
+    import torch
+
+    global _flush_buf
+    if _flush_buf is None:
+        _flush_buf = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda")
+    _flush_buf.fill_(1)
+
+
 def timed_steps(fn, steps, warmup):
     """Untimed calls for SETTLE_S seconds, then W untimed calls, then exactly K
     calls bracketed by synchronize, with one HIP event on the current (launch)
     stream at each step boundary (K+1 events): step i lasts from event i to
     event i+1.  One marker per step, not a start and an end, keeps the events'
     own cost out of short kernels' times.
-    Returns (total_ms, mean_event_ms, median_event_ms)."""
+
+    Then K flushed steps: before each, FLUSH_BYTES are overwritten (untimed),
+    and a start and an end event bracket the call alone (the reference's
+    per-rep protocol, bench/bench.py:44-60).
+
+    Returns dict(total_ms, mean_ms, median_ms, flushed_mean_ms,
+    flushed_median_ms, calls_before_timed): the last is the number of calls
+    made before the first timed one, counted from the caller's first call
+    (which the caller makes before this function), so that a profiler trace
+    can pick out the timed dispatches."""
     import torch
 
+    calls = 1
     settle_end = time.perf_counter() + SETTLE_S
     while time.perf_counter() < settle_end:
         for _ in range(8):
             fn()
+        calls += 8
         torch.cuda.synchronize()
     for _ in range(warmup):
         fn()
+    calls += warmup
     torch.cuda.synchronize()
     marks = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     t0 = time.perf_counter()
@@ -114,7 +146,39 @@ def timed_steps(fn, steps, warmup):
     torch.cuda.synchronize()
     total_ms = (time.perf_counter() - t0) * 1e3
     ev = [a.elapsed_time(b) for a, b in zip(marks[:-1], marks[1:])]
-    return total_ms, sum(ev) / len(ev), statistics.median(ev)
+    flushed = []
+    for _ in range(steps):
+        flush_caches()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        b.synchronize()
+        flushed.append(a.elapsed_time(b))
+    return dict(total_ms=total_ms, mean_ms=sum(ev) / len(ev), median_ms=statistics.median(ev),
+                flushed_mean_ms=sum(flushed) / len(flushed), flushed_median_ms=statistics.median(flushed),
+                calls_before_timed=calls)
+
+
+def timing_fields(t, steps, work, unit):
+    """The per-workload timing columns: `value` from the K back-to-back steps
+    (wall clock), `kernel_*` from their step-boundary events, `flushed` from the
+    K flushed steps; `work` is FLOP (unit TFLOP/s) or bytes (GB/s) per step."""
+    scale, peak = (1e12, PEAK_FP16_TFLOPS) if unit == "TFLOP/s" else (1e9, PEAK_HBM_GBS)
+
+    def rate(ms):
+        return work / (ms * 1e-3) / scale
+
+    ms = t["total_ms"] / steps
+    key = "kernel_tflops" if unit == "TFLOP/s" else "kernel_gbs"
+    return {"value": round(rate(ms), 2), "unit": unit, "ms_per_step": round(ms, 4),
+            "kernel_ms_mean": round(t["mean_ms"], 4), "kernel_ms_median": round(t["median_ms"], 4),
+            key: round(rate(t["mean_ms"]), 2), "frac_of_peak": round(rate(t["mean_ms"]) / peak, 4),
+            "flushed": {"flush_bytes": FLUSH_BYTES, "steps": steps, "kernel_ms_mean": round(t["flushed_mean_ms"], 4),
+                        "kernel_ms_median": round(t["flushed_median_ms"], 4),
+                        "value": round(rate(t["flushed_median_ms"]), 2), "unit": unit,
+                        "frac_of_peak": round(rate(t["flushed_median_ms"]) / peak, 4)},
+            "calls_before_timed": t["calls_before_timed"]}
 
 
 def prefill_case(b, h, n, d, causal, steps, warmup, seed=0):
@@ -131,15 +195,10 @@ def prefill_case(b, h, n, d, causal, steps, warmup, seed=0):
     ref = torch_attention_fp32(q[0, 0], k[0, 0], v[0, 0], causal, d ** -0.5)
     err = float((out[0, 0].float() - ref).abs().max())
     del out, ref
-    total_ms, ev_mean, ev_med = timed_steps(fn, steps, warmup)
+    t = timed_steps(fn, steps, warmup)
     flops = prefill_flops(b, h, n, d, causal)
-    ms = total_ms / steps
     res = dict(workload=f"prefill B={b} H={h} N={n} D={d} {'causal' if causal else 'non-causal'}",
-               value=round(flops / (ms * 1e-3) / 1e12, 2), unit="TFLOP/s", ms_per_step=round(ms, 4),
-               kernel_ms_mean=round(ev_mean, 4), kernel_ms_median=round(ev_med, 4),
-               kernel_tflops=round(flops / (ev_mean * 1e-3) / 1e12, 2),
-               frac_of_peak=round(flops / (ev_mean * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
-               flop_per_launch=flops, max_abs_err=float(f"{err:.3g}"))
+               **timing_fields(t, steps, flops, "TFLOP/s"), flop_per_launch=flops, max_abs_err=float(f"{err:.3g}"))
     del q, k, v
     torch.cuda.empty_cache()
     return res
@@ -184,16 +243,12 @@ def decode_case(lens, hkv, d, bs, partition, steps, warmup, seed=0, hq=None):
         ref = torch_attention_fp32(q[0, kvh * grp:(kvh + 1) * grp], kseq[kvh], vseq[kvh], False, d ** -0.5)
         err = max(err, float((out[0, kvh * grp:(kvh + 1) * grp].float() - ref).abs().max()))
     del out, kseq, vseq
-    total_ms, ev_mean, ev_med = timed_steps(fn, steps, warmup)
+    t = timed_steps(fn, steps, warmup)
     nbytes = decode_kv_bytes(lens, hkv, d)
-    ms = total_ms / steps
     res = dict(workload=f"paged decode B={len(lens)} Hq={hq} Hkv={hkv} D={d} bs={bs} P={partition} "
                         f"sum_ctx={sum(lens)} max_ctx={max_ctx}",
-               value=round(nbytes / (ms * 1e-3) / 1e9, 1), unit="GB/s", ms_per_step=round(ms, 4),
-               kernel_ms_mean=round(ev_mean, 4), kernel_ms_median=round(ev_med, 4),
-               kernel_gbs=round(nbytes / (ev_mean * 1e-3) / 1e9, 1),
-               frac_of_peak=round(nbytes / (ev_mean * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-               bytes_per_step=nbytes, splits=-(-max_ctx // partition), max_abs_err=float(f"{err:.3g}"))
+               **timing_fields(t, steps, nbytes, "GB/s"), bytes_per_step=nbytes, splits=-(-max_ctx // partition),
+               max_abs_err=float(f"{err:.3g}"))
     del kc, vc, q
     torch.cuda.empty_cache()
     return res
@@ -220,16 +275,11 @@ def varlen_case(lens, h, hkv, d, causal, steps, warmup, seed=0):
     err = max(float((out[:n0, hh].float() - torch_attention_fp32(q[:n0, hh], k[:n0, 0], v[:n0, 0], causal,
                                                                 d ** -0.5)).abs().max()) for hh in range(2))
     del out
-    total_ms, ev_mean, ev_med = timed_steps(fn, steps, warmup)
+    t = timed_steps(fn, steps, warmup)
     flops = sum(prefill_flops(1, h, n, d, causal) for n in lens)
-    ms = total_ms / steps
     res = dict(workload=f"varlen prefill {len(lens)} seqs total={total} max={max(lens)} H={h} Hkv={hkv} D={d} "
                         f"{'causal' if causal else 'non-causal'}",
-               value=round(flops / (ms * 1e-3) / 1e12, 2), unit="TFLOP/s", ms_per_step=round(ms, 4),
-               kernel_ms_mean=round(ev_mean, 4), kernel_ms_median=round(ev_med, 4),
-               kernel_tflops=round(flops / (ev_mean * 1e-3) / 1e12, 2),
-               frac_of_peak=round(flops / (ev_mean * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
-               flop_per_launch=flops, max_abs_err=float(f"{err:.3g}"))
+               **timing_fields(t, steps, flops, "TFLOP/s"), flop_per_launch=flops, max_abs_err=float(f"{err:.3g}"))
     del q, k, v
     torch.cuda.empty_cache()
     return res
@@ -262,15 +312,10 @@ def cache_write_case(tokens, hkv, d, bs, steps, warmup, seed=0):
     unused = torch.ones(pool, dtype=torch.bool, device="cuda")
     unused[torch.from_numpy(pages).cuda()] = False
     mism += int(kc[unused].count_nonzero()) + int(vc[unused].count_nonzero())
-    total_ms, ev_mean, ev_med = timed_steps(fn, steps, warmup)
+    t = timed_steps(fn, steps, warmup)
     nbytes = 2 * tokens * hkv * d * 2 * 2 + tokens * 8
-    ms = total_ms / steps
     res = dict(workload=f"paged cache write T={tokens} Hkv={hkv} D={d} bs={bs} fp16 (shuffled pages)",
-               value=round(nbytes / (ms * 1e-3) / 1e9, 1), unit="GB/s", ms_per_step=round(ms, 4),
-               kernel_ms_mean=round(ev_mean, 4), kernel_ms_median=round(ev_med, 4),
-               kernel_gbs=round(nbytes / (ev_mean * 1e-3) / 1e9, 1),
-               frac_of_peak=round(nbytes / (ev_mean * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-               bytes_per_step=nbytes, mismatched_elements=mism)
+               **timing_fields(t, steps, nbytes, "GB/s"), bytes_per_step=nbytes, mismatched_elements=mism)
     del key, value, kc, vc
     torch.cuda.empty_cache()
     return res
@@ -394,6 +439,8 @@ def main():
         "decode_long8_d64": lambda: decode_case([32768] * 8, 32, 64, 16, 256, K, W),
         # a Llama-3-8B-like decode layer: 4 query heads per kv head, the default partition
         "decode_gqa16_d128": lambda: decode_case([8192] * 16, 8, 128, 16, None, K, W, hq=32),
+        # 8 query heads per kv head (the heaviest head group the kernels take), default partition
+        "decode_g8_d128": lambda: decode_case([8192] * 8, 8, 128, 16, None, K, W, hq=64),
         # packed prompts of mixed lengths, 4 query heads per kv head, no padding
         "prefill_varlen_gqa": lambda: varlen_case(lensv, 32, 8, 128, True, K, W),
         # the step before decode reads the cache: append a batch of prompts' K/V to it
@@ -424,8 +471,11 @@ def main():
             "bound": "hbm" if hbm else "mfma", "achieved": ach, "peak": peak, "unit": v["unit"],
             "frac": round(ach / peak, 4), "traffic": t["traffic_bytes"] if t else None}))
     cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
+    from attnkernels import build as akbuild
+    digest = akbuild.sources_digest()  # names the kernel sources measured (profiles cite it)
     if headline is None:  # a profiling run of other workloads: report them only
-        print(json.dumps({"workloads": workloads, "cpu_baseline": cpu}), flush=True)
+        print(json.dumps({"workloads": workloads, "steps": K, "warmup": W, "sources_sha256": digest,
+                          "cpu_baseline": cpu}), flush=True)
         return
     ach = headline["kernel_tflops"]
     line = {
@@ -436,6 +486,12 @@ def main():
         "config": {"workload": headline["workload"] + " (BASELINE configs[2])", "global_batch": 2,
                    "seq_len": 8192, "heads": 32, "head_dim": 128, "causal": True, "parallelism": "none"},
         "max_abs_err": headline["max_abs_err"],
+        # the same workload with 512 MiB written before each step (outside the
+        # step's event pair), as the reference times every rep
+        "flushed": headline["flushed"],
+        "kernel_ms_mean": headline["kernel_ms_mean"], "kernel_ms_median": headline["kernel_ms_median"],
+        "flop_per_launch": headline["flop_per_launch"], "calls_before_timed": headline["calls_before_timed"],
+        "sources_sha256": digest,
         "roofline": {"bound": "mfma", "achieved": ach, "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(ach / PEAK_FP16_TFLOPS, 4),
                      "traffic": (measured_traffic("prefill_d128_n8192_causal") or {}).get("traffic_bytes"),

@@ -14,7 +14,9 @@ Two artefacts, both next to this file:
 from __future__ import annotations
 
 import hashlib
+import json
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -61,6 +63,28 @@ def _run(cmd, verbose):
                            f"{r.stdout}\n{r.stderr}")
     if verbose and (r.stdout or r.stderr):
         print(r.stdout, r.stderr, flush=True)
+    return r
+
+
+# Per-kernel resource usage, from the compiler's kernel-resource-usage remarks
+# (VGPRs, AGPRs, spills, LDS, waves per SIMD): read by attnkernels.profiling.
+RESOURCE_USAGE = OBJ / "resource_usage.json"
+_REMARK = re.compile(r"remark:\s+(Function Name|[A-Za-z ]+?)(?: \[[^\]]*\])?: (\S+) \[-Rpass-analysis")
+
+
+def parse_resource_usage(text):
+    """{mangled kernel name: {field: value}} from -Rpass-analysis=kernel-resource-usage output."""
+    out, cur = {}, None
+    for line in text.splitlines():
+        m = _REMARK.search(line)
+        if not m:
+            continue
+        key, val = m.group(1).strip(), m.group(2)
+        if key == "Function Name":
+            cur = out.setdefault(val, {})
+        elif cur is not None:
+            cur[key] = int(val) if val.isdigit() else val
+    return out
 
 
 def build_library(verbose=False, extra_flags=()):
@@ -70,14 +94,18 @@ def build_library(verbose=False, extra_flags=()):
     inc = [f"-I{INCLUDE}", f"-I{CSRC}"]
     jobs = []
     for src in HIP_SOURCES:
-        jobs.append([hipcc, *HIPCC_FLAGS, *extra_flags, *inc, "-c", CSRC / src,
-                     "-o", OBJ / (src + ".o")])
+        jobs.append([hipcc, *HIPCC_FLAGS, *extra_flags, *inc, "-Rpass-analysis=kernel-resource-usage", "-c",
+                     CSRC / src, "-o", OBJ / (src + ".o")])
     for src in CPP_SOURCES:
         jobs.append([hipcc, "-O2", "-std=c++17", "-fPIC", "-Wall", *inc, "-x", "c++",
                      "-D__HIP_PLATFORM_AMD__=1", "-I/opt/rocm/include", "-c",
                      CSRC / src, "-o", OBJ / (src + ".o")])
     with ThreadPoolExecutor(max_workers=len(jobs)) as ex:
-        list(ex.map(lambda c: _run(c, verbose), jobs))
+        results = list(ex.map(lambda c: _run(c, verbose), jobs))
+    usage = {}
+    for r in results:
+        usage.update(parse_resource_usage(r.stderr))
+    RESOURCE_USAGE.write_text(json.dumps(usage, indent=1, sort_keys=True) + "\n")
     objs = [OBJ / (s + ".o") for s in HIP_SOURCES + CPP_SOURCES]
     tmp = LIB.with_suffix(".so.tmp")
     _run([hipcc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp], verbose)

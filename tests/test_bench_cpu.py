@@ -16,7 +16,7 @@ import oracle
 from conftest import ROOT
 
 WORKLOADS = ["prefill_d128_n8192_causal", "prefill_d64_n2048", "prefill_d128_n8191_causal",
-             "decode_ragged64_d128", "decode_long8_d128", "decode_long8_d64", "decode_gqa16_d128",
+             "decode_ragged64_d128", "decode_long8_d128", "decode_long8_d64", "decode_gqa16_d128", "decode_g8_d128",
              "prefill_varlen_gqa", "cache_write_t16k"]
 
 

@@ -1,0 +1,87 @@
+"""attnkernels.profiling on synthetic rocprofv3 output (CPU): only the timed
+dispatches are summarised, picked by bench.py's calls_before_timed, and the
+trace-side step time is the start-to-start period of those steps."""
+import csv
+import json
+
+import pytest
+
+from attnkernels import profiling
+
+HEADER = ["Kind", "Agent_Id", "Queue_Id", "Stream_Id", "Thread_Id", "Dispatch_Id", "Kernel_Id", "Kernel_Name",
+          "Correlation_Id", "Start_Timestamp", "End_Timestamp", "LDS_Block_Size", "Scratch_Size", "VGPR_Count",
+          "Accum_VGPR_Count", "SGPR_Count", "Workgroup_Size_X", "Workgroup_Size_Y", "Workgroup_Size_Z",
+          "Grid_Size_X", "Grid_Size_Y", "Grid_Size_Z"]
+DEC = "void ak::paged_decode_kernel<128, 4>(_Float16 const*, int)"
+RED = "void ak::paged_reduce_kernel<128>(float const*, int)"
+
+
+def write_trace(path, calls):
+    """calls: list of [(name, start, end)] per bench.py call; torch kernels in between."""
+    rows, did = [], 0
+    for kernels in calls:
+        did += 1
+        rows.append(["KERNEL_DISPATCH"] + [""] * 4 + [did, 1, "void at::native::fill_kernel()", did, 0, 1] +
+                    [""] * 11)
+        for name, s, e in kernels:
+            did += 1
+            rows.append(["KERNEL_DISPATCH"] + [""] * 4 + [did, 2, name, did, s, e] + [""] * 11)
+    with open(path, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(HEADER)
+        w.writerows(rows)
+
+
+def test_short_names():
+    assert profiling.short_name(DEC) == "paged_decode_kernel<128,4>"
+    assert profiling.short_name("_ZN2ak20flash_prefill_kernelILi128ELb1ELb0ELi8EEEvPKDF16_") == \
+        "flash_prefill_kernel<128,true,false,8>"
+    assert not profiling.ours("void at::native::fill_kernel()")
+
+
+def test_trace_summary_takes_only_the_timed_steps(tmp_path):
+    n0, K = 7, 5
+    calls, t = [], 0
+    for i in range(n0 + 2 * K):
+        slow = i < n0  # settle / warmup calls are slower: they must not enter the stats
+        d = 300_000 if slow else 100_000 + 1000 * (i - n0)
+        calls.append([(DEC, t, t + d), (RED, t + d + 2000, t + d + 7000)])
+        t += d + 10_000
+    raw = tmp_path / "raw"
+    raw.mkdir()
+    write_trace(raw / "trace_kernel_trace.csv", calls)
+    rec = {"name": "decode_x", "workload": "paged decode test", "unit": "GB/s", "bytes_per_step": 1e9,
+           "calls_before_timed": n0, "kernel_ms_mean": 0.112, "kernel_ms_median": 0.112, "ms_per_step": 0.113,
+           "kernel_gbs": 8900.0, "frac_of_peak": 1.1}
+    (raw / "bench_trace.json").write_text(json.dumps({"workloads": [rec], "steps": K, "warmup": 2,
+                                                      "sources_sha256": "0" * 64}) + "\n")
+    out_dir = tmp_path / "profiles"
+    out_dir.mkdir()
+    out, dom, st, step = profiling.trace_summary("decode_x", raw, out_dir)
+    assert dom == "paged_decode_kernel<128,4>"
+    assert st["n"] == K
+    assert st["mean"] == pytest.approx(102.0)          # 100..104 us, the settle calls excluded
+    assert st["median"] == pytest.approx(102.0)
+    assert step == pytest.approx(101.5 + 10.0)         # K-1 start-to-start periods: 100..103 us + 10 us gap
+    text = out.read_text()
+    assert "dispatches #7..#11" in text and "flushed median" in text
+
+
+def test_trace_summary_refuses_a_short_trace(tmp_path):
+    raw = tmp_path / "raw"
+    raw.mkdir()
+    write_trace(raw / "trace_kernel_trace.csv", [[(DEC, 0, 10)]] * 3)
+    (raw / "bench_trace.json").write_text(json.dumps({"workloads": [{"name": "w", "calls_before_timed": 2,
+                                                                     "unit": "GB/s"}], "steps": 5}) + "\n")
+    with pytest.raises(SystemExit):
+        profiling.trace_summary("w", raw, tmp_path)
+
+
+def test_resource_usage_remarks_parse():
+    from attnkernels import build
+    text = """x.hip:80:1: remark: Function Name: _ZN2ak19paged_decode_kernelILi64ELi1EEEv [-Rpass-analysis=kernel-resource-usage]
+x.hip:80:1: remark:     VGPRs: 60 [-Rpass-analysis=kernel-resource-usage]
+x.hip:80:1: remark:     Occupancy [waves/SIMD]: 8 [-Rpass-analysis=kernel-resource-usage]
+x.hip:80:1: remark:     LDS Size [bytes/block]: 2112 [-Rpass-analysis=kernel-resource-usage]"""
+    u = build.parse_resource_usage(text)
+    assert u == {"_ZN2ak19paged_decode_kernelILi64ELi1EEEv": {"VGPRs": 60, "Occupancy": 8, "LDS Size": 2112}}
