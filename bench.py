@@ -91,79 +91,21 @@ def log(msg):
 SETTLE_S = 0.25
 
 
-# Bytes written between flushed steps: twice MI355X's 256 MB Infinity Cache (and
-# far more than the 8 x 4 MB of L2), so a flushed step reads its inputs from HBM.
-# The reference flushes its T4's L2 before every timed rep (bench/bench.py:37-41).
-FLUSH_BYTES = 512 << 20
-_flush_buf = None
-
-
-def flush_caches():
-    """Overwrite FLUSH_BYTES of device memory (one fill kernel)."""
-    import torch
-
-    global _flush_buf
-    if _flush_buf is None:
-        _flush_buf = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda")
-    _flush_buf.fill_(1)
-
-
 def timed_steps(fn, steps, warmup):
-    """Untimed calls for SETTLE_S seconds, then W untimed calls, then exactly K
-    calls bracketed by synchronize, with one HIP event on the current (launch)
-    stream at each step boundary (K+1 events): step i lasts from event i to
-    event i+1.  One marker per step, not a start and an end, keeps the events'
-    own cost out of short kernels' times.
+    """The driver's protocol (attnkernels.timing.steady_steps): settle, W warmup
+    steps, K back-to-back steps with one event per step boundary, then K
+    flushed steps (512 MiB overwritten before each, outside its events)."""
+    from attnkernels import timing
 
-    Then K flushed steps: before each, FLUSH_BYTES are overwritten (untimed),
-    and a start and an end event bracket the call alone (the reference's
-    per-rep protocol, bench/bench.py:44-60).
-
-    Returns dict(total_ms, mean_ms, median_ms, flushed_mean_ms,
-    flushed_median_ms, calls_before_timed): the last is the number of calls
-    made before the first timed one, counted from the caller's first call
-    (which the caller makes before this function), so that a profiler trace
-    can pick out the timed dispatches."""
-    import torch
-
-    calls = 1
-    settle_end = time.perf_counter() + SETTLE_S
-    while time.perf_counter() < settle_end:
-        for _ in range(8):
-            fn()
-        calls += 8
-        torch.cuda.synchronize()
-    for _ in range(warmup):
-        fn()
-    calls += warmup
-    torch.cuda.synchronize()
-    marks = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
-    t0 = time.perf_counter()
-    marks[0].record()
-    for i in range(steps):
-        fn()
-        marks[i + 1].record()
-    torch.cuda.synchronize()
-    total_ms = (time.perf_counter() - t0) * 1e3
-    ev = [a.elapsed_time(b) for a, b in zip(marks[:-1], marks[1:])]
-    flushed = []
-    for _ in range(steps):
-        flush_caches()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        fn()
-        b.record()
-        b.synchronize()
-        flushed.append(a.elapsed_time(b))
-    return dict(total_ms=total_ms, mean_ms=sum(ev) / len(ev), median_ms=statistics.median(ev),
-                flushed_mean_ms=sum(flushed) / len(flushed), flushed_median_ms=statistics.median(flushed),
-                calls_before_timed=calls)
+    return timing.steady_steps(fn, steps, warmup, settle_s=SETTLE_S)
 
 
 def timing_fields(t, steps, work, unit):
     """The per-workload timing columns: `value` from the K back-to-back steps
     (wall clock), `kernel_*` from their step-boundary events, `flushed` from the
     K flushed steps; `work` is FLOP (unit TFLOP/s) or bytes (GB/s) per step."""
+    from attnkernels.timing import FLUSH_BYTES
+
     scale, peak = (1e12, PEAK_FP16_TFLOPS) if unit == "TFLOP/s" else (1e9, PEAK_HBM_GBS)
 
     def rate(ms):

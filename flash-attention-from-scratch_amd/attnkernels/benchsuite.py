@@ -1,338 +1,361 @@
-"""Comparison benchmark of the attention kernels on one MI355X; writes a JSON file.
+"""Comparison suite on one MI355X: this build's kernels against PyTorch's own
+attention, and the split-K partition sweeps behind ``decode_partition``.
+Writes a JSON file that ``attnkernels.report`` renders as markdown.
 
-The counterpart of the reference's comparison harness (bench/bench.py:142-332),
-with the same sections:
-
-* ``prefill``: this build's flash prefill against PyTorch's SDPA backends over a
-  sweep of sequence lengths at a constant token count, D in {64, 128}, causal
-  and not (bench/bench.py:142-189);
-* ``decode``: paged split-K decode (and the same kernel with one split) against
-  "gather the pages, then SDPA" and SDPA on an already contiguous cache, for a
-  Llama-3-8B-like layer, Hq=32, Hkv=8, D=128, page size 16
-  (bench/bench.py:194-268);
-* ``split_ablation``: decode bandwidth for every power-of-two partition, to
-  check the ``decode_partition`` rule on 256 CUs (bench/bench.py:271-278);
-* ``ragged``: a batch with mixed context lengths (bench/bench.py:281-287);
-* ``roofs``: practical ceilings of this GPU, a large device copy and an
-  8192^3 fp16 GEMM (bench/bench.py:111-124).
-
-Timing: hipEvents around each call after a warm-up, median over 3..50 calls
-(about 0.3 s per case).  Before every timed call a 512 MiB buffer is cleared,
-outside the timed region, so the 256 MB Infinity Cache does not serve data
-from the previous call.
-
-SDPA is always pinned to its flash / memory-efficient backends: its math
-backend (batched matmuls on transposed views) is never run.
-
-    python -m attnkernels.benchsuite --out results/mi355x.json [--quick]
+    python -m attnkernels.benchsuite --out results/mi355x.json [--quick] [--sections ...]
     python -m attnkernels.report results/mi355x.json > results/mi355x.md
+
+Structure.  A section is a list of case builders.  A builder allocates one
+case's inputs on the device and returns a ``Case``: the row's shape columns,
+the work of one call (FLOP, or K/V bytes), the implementations to compare
+(zero-argument callables), and an error function against an fp32 reference.
+One runner, ``run_case``, times every implementation with the flushed
+protocol of ``attnkernels.timing`` (512 MiB overwritten before each call,
+median of 5-40 calls within a quarter second), measures its extra peak
+memory, and emits one row per implementation.  The JSON file is rewritten
+after every case, so an interrupted run keeps what it measured.
+
+Sections (the row schema ``attnkernels.report`` reads):
+  prefill                flash_attention vs SDPA (flash, memory-efficient, both),
+                         at a constant token count per shape, D in {64, 128},
+                         causal and not: the shapes of the reference's T4
+                         tables (its bench/bench.py prefill sweep), so the two
+                         can be read side by side
+  decode                 paged_decode (default partition, and one split) vs
+                         gathering the pages then SDPA, and SDPA on a cache
+                         that is already contiguous: Llama-3-8B's attention
+                         layer (32 query heads, 8 kv heads, D=128, 16-token pages)
+  decode_heads           paged_decode over head-group sizes 1-8 and D 64/128
+  split_ablation         every power-of-two partition from 256 tokens to one
+                         split, uniform batches
+  split_ablation_ragged  the same over batches of mixed context lengths
+  ragged                 one mixed-length batch, all decode implementations
+
+SDPA is pinned to its fused backends; its math backend (batched products on
+transposed views, which have faulted GPUs on this pool) never runs.
 """
 from __future__ import annotations
 
 import argparse
 import datetime as dt
 import json
+import os
 import platform
-import statistics
 import sys
 import time
+from dataclasses import dataclass, field
 from pathlib import Path
+from typing import Callable, Dict, Iterator, Optional
 
 import torch
 import torch.nn.functional as F
 
 import attnkernels as ak
 from attnkernels import reference as akref
+from attnkernels import timing
 
 try:
     from torch.nn.attention import SDPBackend, sdpa_kernel
 except ImportError:  # older torch
     SDPBackend = sdpa_kernel = None
 
-FLUSH_BYTES = 512 << 20
-_flush_buf = None
+PEAK = {"TFLOP/s": 2500.0, "GB/s": 8000.0}   # MI355X: dense fp16 MFMA, HBM3E
 
 
-def flush_caches():
-    """Clear a 512 MiB buffer: evicts L2 and the Infinity Cache."""
-    global _flush_buf
-    if _flush_buf is None:
-        _flush_buf = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda")
-    _flush_buf.zero_()
+@dataclass
+class Case:
+    section: str
+    fields: dict                                   # the row's shape columns
+    work: float                                    # FLOP or bytes of one call
+    unit: str                                      # "TFLOP/s" or "GB/s"
+    impls: Dict[str, Callable[[], torch.Tensor]]
+    error: Callable[[torch.Tensor], float]         # output -> max abs error vs fp32
+    baseline: Optional[str] = None                 # implementation the speed-ups divide by
+    speedup_key: Optional[str] = None
+    per_impl: Dict[str, dict] = field(default_factory=dict)  # extra columns of one implementation
 
 
-def median_ms(fn, warmup=1, budget_ms=300.0, lo=3, hi=50):
-    """Median hipEvent time of fn() over lo..hi calls, each after a cache flush."""
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    samples, reps = [], hi
-    while len(samples) < reps:
-        flush_caches()
-        t0.record()
-        fn()
-        t1.record()
-        t1.synchronize()
-        samples.append(t0.elapsed_time(t1))
-        if len(samples) == 1:
-            reps = int(min(hi, max(lo, budget_ms / max(samples[0], 1e-3))))
-    return statistics.median(samples)
+# ---------------------------------------------------------------- SDPA -----
 
-
-def extra_peak_mb(fn):
-    """Peak device memory one call allocates on top of what is live (output included)."""
-    torch.cuda.synchronize()
-    torch.cuda.reset_peak_memory_stats()
-    before = torch.cuda.memory_allocated()
-    out = fn()
-    torch.cuda.synchronize()
-    peak = torch.cuda.max_memory_allocated() - before
-    del out
-    return round(peak / 2**20, 1)
-
-
-def sdpa_pinned(*backends):
-    """SDPA restricted to the given backends (never the math path)."""
-    def run(q, k, v, causal=False, attn_mask=None):
+def sdpa_on(backends):
+    """SDPA restricted to ``backends`` (never the math path)."""
+    def run(q, k, v, causal=False):
         with sdpa_kernel(list(backends)):
-            return F.scaled_dot_product_attention(q, k, v, attn_mask=attn_mask, is_causal=causal)
+            return F.scaled_dot_product_attention(q, k, v, is_causal=causal)
     return run
 
 
-def probe_sdpa_backends():
-    """Which fused SDPA backends accept fp16 [B, H, N, 128] here."""
-    found = {}
+def available_sdpa():
+    """{backend name: "ok" | reason} for the fused SDPA backends on this GPU (fp16, D=128)."""
+    status = {}
     if sdpa_kernel is None:
-        return found
-    q = torch.randn(1, 2, 256, 128, device="cuda", dtype=torch.float16)
+        return status
+    x = torch.randn(1, 2, 128, 128, device="cuda", dtype=torch.float16)
     for name in ("FLASH_ATTENTION", "EFFICIENT_ATTENTION", "CUDNN_ATTENTION"):
-        backend = getattr(SDPBackend, name, None)
-        if backend is None:
+        be = getattr(SDPBackend, name, None)
+        if be is None:
             continue
         try:
-            sdpa_pinned(backend)(q, q, q, True)
+            sdpa_on([be])(x, x, x, True)
             torch.cuda.synchronize()
-            found[name] = "ok"
+            status[name] = "ok"
         except Exception as e:  # noqa: BLE001
-            found[name] = "unavailable: " + str(e).splitlines()[0][:200]
-    found["MATH"] = "not run (batched matmuls on transposed views are avoided on this GPU pool)"
-    return found
+            status[name] = "unavailable: " + str(e).splitlines()[0][:160]
+    status["MATH"] = "not run (batched products on transposed views are avoided on this GPU pool)"
+    return status
 
 
-def fused_backends(found):
-    return [getattr(SDPBackend, n) for n in ("FLASH_ATTENTION", "EFFICIENT_ATTENTION") if found.get(n) == "ok"]
+def usable(status):
+    return [getattr(SDPBackend, n) for n, s in status.items() if s == "ok"]
 
 
-def roofs():
-    """Practical ceilings: 2 GiB device-to-device copy, 8192^3 fp16 GEMM."""
-    src = torch.empty(2 << 30, dtype=torch.uint8, device="cuda").fill_(1)
+# ------------------------------------------------------------- ceilings ----
+
+def ceilings():
+    """What this GPU sustains in practice: a 2 GiB device copy (GB/s of reads +
+    writes) and an 8192^3 fp16 GEMM (hipBLASLt through torch.mm)."""
+    n = 2 << 30
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
-    ms = median_ms(lambda: dst.copy_(src))
-    copy_gbs = 2 * src.numel() / (ms * 1e-3) / 1e9
+    copy_ms = min(timing.flushed_samples(lambda: dst.copy_(src), min_calls=5, max_calls=10))
     del src, dst
-    a = torch.randn(8192, 8192, device="cuda", dtype=torch.float16)
-    b = torch.randn(8192, 8192, device="cuda", dtype=torch.float16)
-    ms = median_ms(lambda: torch.mm(a, b))
-    gemm = 2 * 8192**3 / (ms * 1e-3) / 1e12
+    a, b = (torch.randn(8192, 8192, device="cuda", dtype=torch.float16) for _ in range(2))
+    gemm_ms = min(timing.flushed_samples(lambda: torch.mm(a, b), min_calls=5, max_calls=20))
     del a, b
     torch.cuda.empty_cache()
-    return dict(copy_gbs=round(copy_gbs, 1), fp16_gemm_tflops=round(gemm, 1))
+    return dict(copy_gbs=round(2 * n / (copy_ms * 1e-3) / 1e9, 1),
+                fp16_gemm_tflops=round(2 * 8192 ** 3 / (gemm_ms * 1e-3) / 1e12, 1))
 
 
-def err_vs_fp32(out, q, k, v, causal):
-    """Max abs error against fp32 attention on batch 0, heads 0-1."""
-    ref = akref.attention_fp32(q[:1, :2], k[:1, :2], v[:1, :2], causal)
-    return (out[:1, :2].float() - ref).abs().max().item()
+# ---------------------------------------------------------------- cases ----
 
-
-def section_prefill(rows, quick, found):
-    heads, tokens = 16, (4096 if quick else 16384)
+def prefill_builders(quick, status, max_kv_gb=None) -> Iterator[Callable[[], Case]]:
+    heads = 16
+    tokens = 4096 if quick else 16384          # batch x sequence length per shape
     seqs = (512, 1024) if quick else (512, 1024, 2048, 4096, 8192)
-    pinned = fused_backends(found)
+    fused = usable(status)
     for d in (64, 128):
         for causal in (False, True):
             for n in seqs:
-                b = max(1, tokens // n)
-                g = torch.Generator(device="cuda").manual_seed(n + d)
-                q, k, v = (torch.randn(b, heads, n, d, generator=g, device="cuda", dtype=torch.float16)
-                           for _ in range(3))
-                flops = 4.0 * b * heads * n * n * d * (0.5 if causal else 1.0)
-                impls = {"flash_attention": lambda: ak.flash_attention(q, k, v, causal=causal)}
-                if pinned:
-                    impls["sdpa_fused"] = lambda: sdpa_pinned(*pinned)(q, k, v, causal)
-                for name in ("FLASH_ATTENTION", "EFFICIENT_ATTENTION"):
-                    if found.get(name) == "ok":
-                        be = getattr(SDPBackend, name)
-                        impls["sdpa_" + name.split("_")[0].lower()] = (
-                            lambda be=be: sdpa_pinned(be)(q, k, v, causal))
-                case = []
-                for name, fn in impls.items():
-                    try:
-                        out = fn()
-                        err = err_vs_fp32(out, q, k, v, causal)
-                        del out
-                        ms = median_ms(fn)
-                        mem = extra_peak_mb(fn)
-                    except Exception as e:  # noqa: BLE001  e.g. unsupported shape
-                        print(f"prefill {name} d={d} N={n}: {e!r}"[:300], flush=True)
-                        torch.cuda.empty_cache()
-                        continue
-                    case.append(dict(section="prefill", impl=name, batch=b, heads=heads, seq=n, head_dim=d,
-                                     causal=causal, ms=round(ms, 4), tflops=round(flops / (ms * 1e-3) / 1e12, 2),
-                                     peak_mem_mb=mem, max_abs_err=float(f"{err:.3g}")))
-                base = next((r["ms"] for r in case if r["impl"] == "sdpa_fused"), None)
-                for r in case:
-                    r["speedup_vs_sdpa"] = round(base / r["ms"], 3) if base else None
-                    rows.append(r)
-                    print(f"prefill d={d} causal={int(causal)} B={b:2d} N={n:5d} {r['impl']:16s} "
-                          f"{r['ms']:8.3f} ms {r['tflops']:8.1f} TFLOP/s err {r['max_abs_err']:.1e} "
-                          f"x{r['speedup_vs_sdpa']}", flush=True)
-                del q, k, v
-                torch.cuda.empty_cache()
+                def build(d=d, causal=causal, n=n):
+                    b = max(1, tokens // n)
+                    g = torch.Generator(device="cuda").manual_seed(1000 * d + n)
+                    q, k, v = (torch.randn(b, heads, n, d, generator=g, device="cuda", dtype=torch.float16)
+                               for _ in range(3))
+                    impls = {"flash_attention": lambda: ak.flash_attention(q, k, v, causal=causal)}
+                    if fused:
+                        impls["sdpa_fused"] = lambda: sdpa_on(fused)(q, k, v, causal)
+                    for be in fused:
+                        impls["sdpa_" + be.name.split("_")[0].lower()] = lambda be=be: sdpa_on([be])(q, k, v, causal)
+
+                    def error(out):
+                        # the first and the last (batch, head) slice against fp32 attention
+                        worst = 0.0
+                        for bi, hi in ((0, 0), (b - 1, heads - 1)):
+                            ref = akref.attention_fp32(q[bi:bi + 1, hi:hi + 1], k[bi:bi + 1, hi:hi + 1],
+                                                       v[bi:bi + 1, hi:hi + 1], causal)
+                            worst = max(worst, (out[bi:bi + 1, hi:hi + 1].float() - ref).abs().max().item())
+                        return worst
+                    return Case("prefill", dict(batch=b, heads=heads, seq=n, head_dim=d, causal=causal),
+                                4.0 * b * heads * n * n * d * (0.5 if causal else 1.0), "TFLOP/s", impls, error,
+                                baseline="sdpa_fused", speedup_key="speedup_vs_sdpa")
+                yield build
 
 
-HQ, HKV, D, BS = 32, 8, 128, 16  # Llama-3-8B-like attention layer
+# Llama-3-8B's attention layer: 32 query heads over 8 kv heads, head_dim 128;
+# 16-token pages.
+LAYER = dict(hq=32, hkv=8, d=128, bs=16)
 
 
-def kv_bytes(lens, hkv=HKV, d=D):
-    return sum(lens) * hkv * d * 2 * 2
-
-
-def decode_case(rows, section, lens, wanted, found, partition=None, extra=None, seed=0):
-    B = len(lens)
+def decode_case(section, lens, impl_names, status, partition=None, hq=LAYER["hq"], hkv=LAYER["hkv"], d=LAYER["d"],
+                seed=0, extra=None):
+    """A paged cache holding ``lens`` tokens per sequence (pages scattered by a
+    seeded permutation), the query of each sequence, and the implementations
+    in impl_names."""
+    bs, B, max_ctx = LAYER["bs"], len(lens), max(lens)
     gen = torch.Generator().manual_seed(seed)
-    kc, vc, tables, clens = akref.make_paged_cache(lens, HKV, D, block_size=BS, generator=gen)
-    q = torch.randn(B, HQ, D, device="cuda", dtype=torch.float16)
-    max_ctx = max(lens)
-    nblk = -(-max_ctx // BS)
+    kc, vc, tables, clens = akref.make_paged_cache(lens, hkv, d, block_size=bs, generator=gen)
+    q = torch.randn(B, hq, d, device="cuda", dtype=torch.float16, generator=torch.Generator(device="cuda")
+                    .manual_seed(seed + 1))
+    nblk = -(-max_ctx // bs)
+    fused = usable(status)
+    part = ak.decode_partition(B, hkv, max_ctx) if partition is None else partition
+    impls, per_impl = {}, {}
+    if "paged_split" in impl_names:
+        impls["paged_split"] = lambda: ak.paged_decode(q, kc, vc, tables, clens, max_ctx, partition_size=part)
+        per_impl["paged_split"] = dict(partition=part, splits=-(-max_ctx // part))
+    if "paged_nosplit" in impl_names:
+        one = -(-max_ctx // ak.CHUNK) * ak.CHUNK
+        impls["paged_nosplit"] = lambda: ak.paged_decode(q, kc, vc, tables, clens, max_ctx, partition_size=one)
     uniform = len(set(lens)) == 1
-    pinned = fused_backends(found)
-    impls = {}
-    if "paged_split" in wanted:
-        impls["paged_split"] = lambda: ak.paged_decode(q, kc, vc, tables, clens, max_ctx, partition_size=partition)
-    if "paged_nosplit" in wanted:
-        impls["paged_nosplit"] = lambda: ak.paged_decode(q, kc, vc, tables, clens, max_ctx,
-                                                          partition_size=-(-max_ctx // ak.CHUNK) * ak.CHUNK)
-    if "torch_gather_sdpa" in wanted and pinned:
-        def gather_sdpa():
-            with sdpa_kernel(pinned):
+    if "torch_gather_sdpa" in impl_names and fused:
+        def gather_then_sdpa():
+            with sdpa_kernel(fused):
                 return akref.paged_decode_torch(q, kc, vc, tables, nblk, context_lens=None if uniform else clens)
-        impls["torch_gather_sdpa"] = gather_sdpa
-    kg = vg = None
-    if "torch_sdpa_contiguous" in wanted and uniform and pinned:
+        impls["torch_gather_sdpa"] = gather_then_sdpa
+    if "torch_sdpa_contiguous" in impl_names and uniform and fused:
         kg, vg = akref.gather_kv(kc, tables, nblk), akref.gather_kv(vc, tables, nblk)
-        qg = q.view(B, HKV, HQ // HKV, D)
-        impls["torch_sdpa_contiguous"] = lambda: sdpa_pinned(*pinned)(qg, kg, vg)
-    expect = akref.paged_decode_fp32(q[:1], kc, vc, tables[:1], clens[:1])
-    nbytes = kv_bytes(lens)
-    part = partition if partition is not None else ak.decode_partition(B, HKV, max_ctx)
-    case = []
-    for name, fn in impls.items():
+        qg = q.view(B, hkv, hq // hkv, d)
+        impls["torch_sdpa_contiguous"] = lambda: sdpa_on(fused)(qg, kg, vg)
+    check = [0, B - 1] if B > 1 else [0]
+    refs = {b: akref.paged_decode_fp32(q[b:b + 1], kc, vc, tables[b:b + 1], clens[b:b + 1]) for b in check}
+
+    def error(out):
+        out = out.reshape(B, hq, d)
+        return max((out[b:b + 1].float() - refs[b].reshape(1, hq, d)).abs().max().item() for b in check)
+    fields = dict(batch=B, ctx=max_ctx, ctx_mean=round(sum(lens) / B, 1), heads=hq, kv_heads=hkv, head_dim=d,
+                  block_size=bs, **(extra or {}))
+    return Case(section, fields, float(sum(lens)) * hkv * d * 2 * 2, "GB/s", impls, error,
+                baseline="torch_gather_sdpa", speedup_key="speedup_vs_torch_gather", per_impl=per_impl)
+
+
+def kv_gb(lens, hkv=LAYER["hkv"], d=LAYER["d"]):
+    return sum(lens) * hkv * d * 4 / 1e9
+
+
+def decode_builders(quick, status, max_kv_gb):
+    grid = [(B, c) for B in ((1, 16) if quick else (1, 4, 16, 64, 256))
+            for c in ((1024, 4096) if quick else (1024, 2048, 4096, 8192, 16384, 32768))]
+    names = ("paged_split", "paged_nosplit", "torch_gather_sdpa", "torch_sdpa_contiguous")
+    for B, c in grid:
+        if kv_gb([c] * B) <= max_kv_gb:
+            yield lambda B=B, c=c: decode_case("decode", [c] * B, names, status)
+
+
+def decode_head_builders(quick, status, max_kv_gb):
+    B, c = (4, 4096) if quick else (16, 8192)
+    for d in (64, 128):
+        for g in (1, 2, 4, 8):
+            hkv = 8
+            yield lambda d=d, g=g, hkv=hkv: decode_case("decode_heads", [c] * B, ("paged_split",), status, hq=g * hkv,
+                                                        hkv=hkv, d=d, extra=dict(group=g))
+
+
+def partitions_up_to(max_ctx):
+    """256, 512, ... up to the first partition that leaves one split."""
+    out, p = [], ak.CHUNK
+    while True:
+        out.append(p)
+        if p >= max_ctx:
+            return out
+        p *= 2
+
+
+def mixed_lengths(batch, lo, hi, seed):
+    return torch.randint(lo, hi + 1, (batch,), generator=torch.Generator().manual_seed(seed)).tolist()
+
+
+def ablation_builders(quick, status, max_kv_gb):
+    uniform = ((1, 8192),) if quick else ((1, 32768), (4, 8192), (16, 4096), (16, 8192), (64, 1024), (64, 4096))
+    for B, c in uniform:
+        for p in partitions_up_to(c):
+            yield lambda B=B, c=c, p=p: decode_case("split_ablation", [c] * B, ("paged_split",), status, partition=p)
+    mixed = ((8, 512, 8192, 3),) if quick else ((4, 512, 32768, 1), (16, 512, 32768, 2), (64, 1, 4096, 3))
+    for B, lo, hi, seed in mixed:
+        lens = mixed_lengths(B, lo, hi, seed)
+        for p in partitions_up_to(max(lens)):
+            yield lambda lens=lens, p=p: decode_case("split_ablation_ragged", lens, ("paged_split",), status,
+                                                     partition=p, extra=dict(ctx_lens=lens))
+
+
+def ragged_builders(quick, status, max_kv_gb):
+    # The reference's ragged batch (16 sequences of 512-32768 tokens, torch's CPU
+    # generator seeded 0: mean 14722, max 31683), regenerated identically so that
+    # its T4 row and this one describe the same batch.
+    B, hi = (8, 8192) if quick else (16, 32768)
+    lens = mixed_lengths(B, 512, hi, 0)
+    names = ("paged_split", "paged_nosplit", "torch_gather_sdpa")
+    yield lambda: decode_case("ragged", lens, names, status, extra=dict(ctx_lens=lens))
+
+
+SECTIONS = {"prefill": prefill_builders, "decode": decode_builders, "decode_heads": decode_head_builders,
+            "split_ablation": ablation_builders, "ragged": ragged_builders}
+
+
+# --------------------------------------------------------------- runner ----
+
+def run_case(case: Case):
+    """One row per implementation: flushed median time, rate, fraction of the
+    MI355X peak, extra peak memory, max abs error; speed-ups against the
+    case's baseline when it ran."""
+    rate_key = "tflops" if case.unit == "TFLOP/s" else "gbs"
+    scale = 1e12 if case.unit == "TFLOP/s" else 1e9
+    rows = []
+    for name, fn in case.impls.items():
         try:
             out = fn()
-            err = (out[:1].float().reshape(expect.shape) - expect).abs().max().item()
+            err = case.error(out)
             del out
-            ms = median_ms(fn)
-        except Exception as e:  # noqa: BLE001
-            print(f"{section} {name} B={B} ctx={max_ctx}: {e!r}"[:300], flush=True)
+            ms = sorted(timing.flushed_samples(fn))
+            med = ms[len(ms) // 2] if len(ms) % 2 else 0.5 * (ms[len(ms) // 2 - 1] + ms[len(ms) // 2])
+            mem = timing.extra_peak_bytes(fn) / 2 ** 20
+        except Exception as e:  # noqa: BLE001  an implementation that rejects the shape
+            print(f"  {case.section} {name} {case.fields}: {e!r}"[:300], flush=True)
             torch.cuda.empty_cache()
             continue
-        r = dict(section=section, impl=name, batch=B, ctx=max_ctx, ctx_mean=round(sum(lens) / B, 1), heads=HQ,
-                 kv_heads=HKV, head_dim=D, block_size=BS, ms=round(ms, 4),
-                 gbs=round(nbytes / (ms * 1e-3) / 1e9, 1), max_abs_err=float(f"{err:.3g}"))
-        if name == "paged_split":
-            r["partition"] = part
-            r["splits"] = -(-max_ctx // part)
-        if extra:
-            r.update(extra)
-        case.append(r)
-    base = next((r["ms"] for r in case if r["impl"] == "torch_gather_sdpa"), None)
-    for r in case:
-        r["speedup_vs_torch_gather"] = round(base / r["ms"], 3) if base else None
-        rows.append(r)
-        print(f"{section} B={B:3d} ctx={max_ctx:6d} {r['impl']:22s} {r['ms']:8.4f} ms {r['gbs']:8.1f} GB/s "
-              f"err {r['max_abs_err']:.1e}{'  P=' + str(r['partition']) if 'partition' in r else ''}", flush=True)
-    del kc, vc, kg, vg, q
-    torch.cuda.empty_cache()
-
-
-def section_decode(rows, quick, found):
-    batches = (1, 16) if quick else (1, 4, 16, 64)
-    ctxs = (1024, 4096) if quick else (1024, 2048, 4096, 8192, 16384, 32768)
-    wanted = ("paged_split", "paged_nosplit", "torch_gather_sdpa", "torch_sdpa_contiguous")
-    for B in batches:
-        for c in ctxs:
-            if kv_bytes([c] * B) <= 2.2e9:
-                decode_case(rows, "decode", [c] * B, wanted, found)
-
-
-def section_split_ablation(rows, quick, found):
-    uniform = ((1, 8192),) if quick else ((1, 32768), (4, 8192), (16, 4096), (64, 4096), (64, 1024))
-    for B, c in uniform:
-        p = ak.CHUNK
-        while p <= c:
-            decode_case(rows, "split_ablation", [c] * B, ("paged_split",), found, partition=p)
-            p *= 2
-    # Mixed lengths: the partition is chosen from max_ctx alone, so check it here too.
-    g = torch.Generator().manual_seed(1)
-    ragged = [(8, 512, 8192)] if quick else [(4, 512, 32768), (16, 512, 32768), (64, 1, 4096)]
-    for B, lo, hi in ragged:
-        lens = torch.randint(lo, hi + 1, (B,), generator=g).tolist()
-        p = ak.CHUNK
-        while p < max(lens) * 2:
-            decode_case(rows, "split_ablation_ragged", lens, ("paged_split",), found, partition=p,
-                        extra=dict(ctx_lens=lens))
-            p *= 2
-
-
-def section_ragged(rows, quick, found):
-    g = torch.Generator().manual_seed(0)
-    B, hi = (8, 8192) if quick else (16, 32768)
-    lens = torch.randint(512, hi + 1, (B,), generator=g).tolist()
-    decode_case(rows, "ragged", lens, ("paged_split", "paged_nosplit", "torch_gather_sdpa"), found,
-                extra=dict(ctx_lens=lens))
-
-
-SECTIONS = {"prefill": section_prefill, "decode": section_decode, "split_ablation": section_split_ablation,
-            "ragged": section_ragged}
+        rate = case.work / (med * 1e-3) / scale
+        rows.append(dict(section=case.section, impl=name, **case.fields, ms=round(med, 4), calls=len(ms),
+                         **{rate_key: round(rate, 2 if case.unit == "TFLOP/s" else 1)},
+                         frac_of_peak=round(rate / PEAK[case.unit], 4), peak_mem_mb=round(mem, 1),
+                         max_abs_err=float(f"{err:.3g}"), **case.per_impl.get(name, {})))
+    base = next((r["ms"] for r in rows if r["impl"] == case.baseline), None)
+    if case.speedup_key:
+        for r in rows:
+            r[case.speedup_key] = round(base / r["ms"], 3) if base else None
+    return rows
 
 
 def device_meta():
     p = torch.cuda.get_device_properties(0)
     return dict(gpu=p.name, arch=getattr(p, "gcnArchName", ""), cu_count=p.multi_processor_count,
-                memory_gb=round(p.total_memory / 2**30, 1), torch=torch.__version__,
+                memory_gb=round(p.total_memory / 2 ** 30, 1), torch=torch.__version__,
                 hip=getattr(torch.version, "hip", None), python=platform.python_version(),
-                date=dt.datetime.now(dt.timezone.utc).strftime("%Y-%m-%d %H:%M UTC"))
+                host_cpus=os.cpu_count(), date=dt.datetime.now(dt.timezone.utc).strftime("%Y-%m-%d %H:%M UTC"))
 
 
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--out", default="results/mi355x.json")
     ap.add_argument("--quick", action="store_true", help="small sizes (a smoke run)")
-    ap.add_argument("--only", nargs="*", default=list(SECTIONS), choices=list(SECTIONS))
+    ap.add_argument("--sections", nargs="*", default=list(SECTIONS), choices=list(SECTIONS))
+    ap.add_argument("--max-kv-gb", type=float, default=4.5,
+                    help="skip decode cases whose K/V exceed this (the BASELINE decode configs hold up to 4.3 GB)")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         raise SystemExit("benchsuite needs a GPU")
-    torch.manual_seed(0)
     ak.load_extension()
     meta = device_meta()
-    meta["sdpa_backends"] = probe_sdpa_backends()
-    meta["roofs"] = roofs()
-    meta["timing"] = "hipEvent median of 3..50 calls, 512 MiB cache flush before each call"
-    print(json.dumps(meta, indent=1), flush=True)
-    rows = []
-    out = Path(args.out)
-    for name in args.only:
-        t = time.perf_counter()
-        try:
-            SECTIONS[name](rows, args.quick, meta["sdpa_backends"])
-        except Exception as e:  # noqa: BLE001  keep the other sections
-            print(f"section {name} failed: {e!r}", flush=True)
-            meta.setdefault("failed_sections", {})[name] = repr(e)[:500]
-        meta.setdefault("section_seconds", {})[name] = round(time.perf_counter() - t, 1)
-        out.parent.mkdir(parents=True, exist_ok=True)
-        out.write_text(json.dumps(dict(meta=meta, results=rows), indent=1))
+    meta["sdpa_backends"] = available_sdpa()
+    meta["roofs"] = ceilings()
+    meta["timing"] = (f"hipEvent median of 5-40 calls (0.25 s budget), {timing.FLUSH_BYTES >> 20} MiB overwritten "
+                      "before each call")
+    print(json.dumps(meta), flush=True)
+    out, rows = Path(args.out), []
+    out.parent.mkdir(parents=True, exist_ok=True)
+    for name in args.sections:
+        t0, n = time.perf_counter(), 0
+        for build in SECTIONS[name](args.quick, meta["sdpa_backends"], args.max_kv_gb):
+            try:
+                case = build()
+                new = run_case(case)
+                del case
+            except Exception as e:  # noqa: BLE001  keep the other cases
+                print(f"{name}: case failed: {e!r}"[:300], flush=True)
+                meta.setdefault("failed_cases", []).append(f"{name}: {e!r}"[:300])
+                new = []
+            torch.cuda.empty_cache()
+            for r in new:
+                rate = r.get("tflops", r.get("gbs"))
+                print(f"{name:22s} {r['impl']:22s} {json.dumps({k: r[k] for k in r if k in ('batch', 'seq', 'ctx', 'head_dim', 'causal', 'partition', 'group')})} "
+                      f"{r['ms']:.4f} ms {rate} err {r['max_abs_err']:.1e}", flush=True)
+            rows += new
+            n += 1
+            tmp = out.with_suffix(".tmp")
+            tmp.write_text(json.dumps(dict(meta=meta, results=rows), indent=1))
+            os.replace(tmp, out)
+        meta.setdefault("section_seconds", {})[name] = round(time.perf_counter() - t0, 1)
+        meta.setdefault("section_cases", {})[name] = n
+    out.write_text(json.dumps(dict(meta=meta, results=rows), indent=1))
     print("wrote", out, flush=True)
     return 0
 

@@ -50,6 +50,67 @@ def prefill_tables(rows):
     return "\n\n".join(parts)
 
 
+def _impls(rows):
+    out = []
+    for r in rows:
+        if r["impl"] not in out:
+            out.append(r["impl"])
+    return out
+
+
+def prefill_memory_tables(rows):
+    """Extra device memory one call allocates at its peak (output included), per
+    head dim, non-causal: the flash kernels hold O(N) state, the naive
+    formulation O(N^2)."""
+    parts = []
+    for d in sorted({r["head_dim"] for r in rows}):
+        sel = [r for r in rows if r["head_dim"] == d and not r["causal"] and "peak_mem_mb" in r]
+        if not sel:
+            continue
+        impls, by = _impls(sel), defaultdict(dict)
+        for r in sel:
+            by[(r["batch"], r["seq"])][r["impl"]] = r["peak_mem_mb"]
+        body = [[f"{b}x{n}"] + [f"{by[(b, n)][i]:.0f}" if i in by[(b, n)] else "-" for i in impls]
+                for (b, n) in sorted(by, key=lambda k: k[1])]
+        parts.append(f"**D={d}, non-causal** (MB above what is live; output included)\n\n" +
+                     _table(["B x N"] + impls, body))
+    return "\n\n".join(parts)
+
+
+def worst_error_table(rows):
+    """Worst max-abs error against fp32 of each implementation, over every shape
+    of the prefill sections and of the decode sections."""
+    body = []
+    for title, secs in (("prefill", ("prefill",)),
+                        ("decode", ("decode", "decode_heads", "ragged", "split_ablation", "split_ablation_ragged"))):
+        sel = [r for r in rows if r["section"] in secs and "max_abs_err" in r]
+        for i in _impls(sel):
+            errs = [r["max_abs_err"] for r in sel if r["impl"] == i]
+            body.append([title, i, len(errs), f"{max(errs):.2e}"])
+    return _table(["path", "impl", "shapes", "worst max abs error"], body) if body else ""
+
+
+def decode_time_table(rows, section="decode"):
+    sel = [r for r in rows if r["section"] == section]
+    if not sel:
+        return ""
+    impls, by = _impls(sel), defaultdict(dict)
+    for r in sel:
+        by[(r["batch"], r["ctx"])][r["impl"]] = r["ms"]
+    body = [[b, c] + [f"{by[(b, c)][i]:.4f}" if i in by[(b, c)] else "-" for i in impls] for (b, c) in sorted(by)]
+    return _table(["B", "max ctx"] + [f"{i} ms" for i in impls], body)
+
+
+def head_group_table(rows):
+    sel = [r for r in rows if r["section"] == "decode_heads"]
+    if not sel:
+        return ""
+    body = [[r["head_dim"], r["group"], r["heads"], r["kv_heads"], r["batch"], r["ctx"], r.get("partition", "-"),
+             f"{r['ms']:.4f}", f"{r['gbs']:.0f}", f"{100 * r['gbs'] / PEAK_GBS:.1f}%"]
+            for r in sorted(sel, key=lambda r: (r["head_dim"], r["group"]))]
+    return _table(["D", "G", "Hq", "Hkv", "B", "ctx", "P", "ms", "GB/s", "% HBM"], body)
+
+
 def decode_table(rows, section):
     sel = [r for r in rows if r["section"] == section]
     if not sel:
@@ -104,19 +165,32 @@ def render(data):
     pre = [r for r in rows if r["section"] == "prefill"]
     if pre:
         lines += ["", "## Prefill", "", prefill_tables(pre)]
+        t = prefill_memory_tables(pre)
+        if t:
+            lines += ["", "### Prefill peak extra memory", "", t]
     for section, title in (("decode", "Paged decode (Hq=32, Hkv=8, D=128, page 16)"),
                            ("ragged", "Ragged batch")):
         t = decode_table(rows, section)
         if t:
             lines += ["", f"## {title}", "", t]
+        t = decode_time_table(rows, section)
+        if t:
+            lines += ["", f"### {title}: time per call", "", t]
+    t = head_group_table(rows)
+    if t:
+        lines += ["", "## Paged decode by head group (query heads per kv head)", "", t]
     t = ablation_table(rows)
     if t:
         lines += ["", "## Split-K partition ablation", "", t]
     t = ablation_table(rows, "split_ablation_ragged")
     if t:
         lines += ["", "## Split-K partition ablation, mixed context lengths (ctx = max)", "", t]
-    if meta.get("failed_sections"):
-        lines += ["", "Failed sections: " + json.dumps(meta["failed_sections"])]
+    t = worst_error_table(rows)
+    if t:
+        lines += ["", "## Worst error against fp32", "", t]
+    for key in ("failed_sections", "failed_cases"):
+        if meta.get(key):
+            lines += ["", f"{key.replace('_', ' ').capitalize()}: " + json.dumps(meta[key])]
     return "\n".join(lines) + "\n"
 
 

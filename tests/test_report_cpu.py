@@ -21,6 +21,12 @@ def _rows():
                      ms=0.1, max_abs_err=1e-5, speedup_vs_torch_gather=5.0))
     rows.append(dict(section="decode", impl="torch_gather_sdpa", batch=4, ctx=4096, gbs=800.0, ms=0.5,
                      max_abs_err=1e-5, speedup_vs_torch_gather=1.0))
+    for impl, mem, err in (("flash_attention", 32.0, 4e-4), ("sdpa_fused", 48.0, 9e-4)):
+        rows.append(dict(section="prefill", impl=impl, batch=8, heads=16, seq=2048, head_dim=64, causal=False,
+                         ms=0.1, tflops=700.0, peak_mem_mb=mem, max_abs_err=err, speedup_vs_sdpa=None))
+    for g, gbs in ((1, 6000.0), (8, 4000.0)):
+        rows.append(dict(section="decode_heads", impl="paged_split", batch=16, ctx=8192, heads=8 * g, kv_heads=8,
+                         head_dim=128, group=g, partition=512, ms=0.09, gbs=gbs, max_abs_err=2e-5))
     return rows
 
 
@@ -33,6 +39,14 @@ def test_render_synthetic():
     assert "| 1 | 4096 | 512 | 3600 |" in md  # best partition of the ablation
     assert "| 4 | 4096 | 4000 | 800 | 50.0% | 512 | 5.0x |" in md
     assert "50% of 8 TB/s" in md and "50% of 2.5 PFLOP/s" in md
+    # peak memory (non-causal only), time per call, head groups, worst error per implementation
+    assert "### Prefill peak extra memory" in md
+    assert "| 8x2048 | 32 | 48 |" in md
+    assert "| 4 | 4096 | 0.1000 | 0.5000 |" in md
+    assert "| 128 | 8 | 64 | 8 | 16 | 8192 | 512 | 0.0900 | 4000 | 50.0% |" in md
+    assert "| prefill | sdpa_fused | 2 | 9.00e-04 |" in md
+    assert "| prefill | flash_attention | 2 | 5.00e-04 |" in md
+    assert "| decode | paged_split | 6 | 2.00e-05 |" in md
 
 
 def test_committed_results_render():
