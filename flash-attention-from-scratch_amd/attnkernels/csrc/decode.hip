@@ -9,25 +9,21 @@
 // reduce merges partials with M = max m_s, w_s = l_s 2^(m_s - M),
 // O = sum w_s o_s / sum w_s.
 //
-// The kernel is built for HBM bandwidth, with no matrix cores:
-//   * a token row of one page is D*2 contiguous bytes; D/8 lanes cover it with
-//     one 16-byte load each, so one wave-wide load reads 4 (D=128) or 8 (D=64)
-//     tokens = 1 KB; a D=128 lane keeps 16 K loads and 16 V loads in flight (4
-//     waves per workgroup; with head groups 8 and 8, or 4 and 4 with 4 query
-//     heads per kv head), a D=64 lane 4 and 4 (8 waves with one query head per
-//     kv head, 4 with head groups): the fastest shape of each head size on
-//     ragged and long-context paged caches, as measured on MI355X;
-//   * the dot product is v_dot2_f32_f16 on the raw fp16 q and k, reduced over
-//     the D/8 lanes of a token with DPP row permutes, then scaled by
-//     scale*log2(e) in fp32;
-//   * each group of D/8 lanes runs its own online softmax over the tokens it
-//     loads (no cross-lane traffic in the loop); the groups of a wave and the
-//     waves of a workgroup are merged once, at the end, by the same LSE rule;
-//   * with head groups and 16-token pages, a wave's chunk is 1, 2 or 4 whole
-//     pages: their ids are wave-uniform scalar loads and each K/V load is a
-//     page base plus a lane offset plus an immediate, with no per-token page
-//     arithmetic or masking; the context's tail, other page sizes and
-//     out-of-range page ids take the checked per-token loads.
+// Both kernels are built for HBM bandwidth, with no matrix cores:
+//   * a token row of one page is D*2 contiguous bytes; D/8 lanes (a lane
+//     group) cover it with one 16-byte load each, so one wave-wide load reads 4
+//     (D=128) or 8 (D=64) tokens = 1 KB;
+//   * the dot products are v_dot2_f32_f16 on the raw fp16 q and k, scaled by
+//     scale*log2(e) in fp32 afterwards;
+//   * with one query head per kv head (paged_decode_kernel) a D=128 lane keeps
+//     16 K loads and 16 V loads in flight, a D=64 lane 4 and 4; each lane
+//     group reduces its dot products with a DPP tree and runs its own online
+//     softmax over the tokens it loads;
+//   * with head groups (paged_decode_gqa_kernel, below) the arithmetic per
+//     byte grows G-fold, and the lane groups share the reduction, the
+//     exponentials and P V out by a butterfly (see there);
+//   * the lane groups of a wave and the waves of a workgroup are merged once,
+//     at the end, by the same LSE rule.
 #include "attn_kernels.hpp"
 #include "wave.hpp"
 
@@ -36,28 +32,15 @@
 
 namespace ak {
 
-template <int D, int G>
+// One query head per kv head (the reference's decode configurations).
+template <int D>
 struct DecodeTile {
-    // Waves per workgroup.  With head groups a workgroup's fixed costs (page
-    // ids, then K/V, before any work; the merge at the end) grow with G while
-    // fewer of them fit on a CU, so D=64 takes 4 waves there: a 256-token
-    // split is then 2 pipelined chunks per wave instead of 1 (1.1-2.1x at the
-    // default partition on MI355X, equal at the best one).
-    static constexpr int NW = D == 128 || G >= 2 ? 4 : 8;
+    static constexpr int NW = D == 128 ? 4 : 8;  // waves per workgroup
     static constexpr int THREADS = NW * kWave;   // 256 or 512
     static constexpr int LPT = D / 8;            // lanes per token row
     static constexpr int TPL = kWave / LPT;      // tokens per wave-wide load
-    // Loads in flight per lane, per cache.  D=128 with head groups spends the
-    // registers on q and the accumulators instead, for more waves per SIMD: 8
-    // with 2 query heads per kv head (127 VGPRs, 4 waves, against 229 and 2 at
-    // 16) and with 8; 4 with 4 (115 VGPRs, 4 waves, against 162 and 3 at 8).
-    static constexpr int U = D == 128 ? (G == 1 ? 16 : G == 4 ? 4 : 8) : 4;
-    static constexpr int TOK = U * TPL;         // tokens per wave iteration
-    // Page size of the fast path: a wave iteration then covers PPI whole pages
-    // (its first token is a multiple of TOK, itself a multiple of 16).
-    static constexpr int FAST_BS = 16;
-    static constexpr int PPI = TOK / FAST_BS;
-    static_assert(TOK % FAST_BS == 0 && FAST_BS % TPL == 0, "whole pages per wave iteration");
+    static constexpr int U = D == 128 ? 16 : 4;  // loads in flight per lane, per cache
+    static constexpr int TOK = U * TPL;          // tokens per wave iteration
 };
 
 __device__ __forceinline__ float dot8(f16x8 a, f16x8 b) {
@@ -71,14 +54,15 @@ __device__ __forceinline__ float dot8(f16x8 a, f16x8 b) {
     return s;
 }
 
-template <int D, int G>
-__global__ void __launch_bounds__((DecodeTile<D, G>::THREADS))
+template <int D>
+__global__ void __launch_bounds__((DecodeTile<D>::THREADS))
 paged_decode_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const f16* __restrict__ vc,
                     const int* __restrict__ block_tables, const int* __restrict__ ctx_lens,
                     f16* __restrict__ out, float* __restrict__ o_part, float* __restrict__ m_part,
                     float* __restrict__ l_part, int hkv, int bs, int bs_shift, int max_blocks,
                     int num_blocks, int partition, int num_splits, float sl2) {
-    using T = DecodeTile<D, G>;
+    using T = DecodeTile<D>;
+    constexpr int G = 1;
     __shared__ float red_acc[T::NW][G][D];
     __shared__ float red_m[T::NW][G], red_l[T::NW][G];
 
@@ -107,120 +91,30 @@ paged_decode_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const
     // the page loads are bounded by the table row, not by the (not yet known)
     // context length, which only masks them afterwards.
     const int ctx_raw = ctx_lens[b];
-    f16x8 qv[G];  // q of the G heads of this kv head, raw fp16 (scaled after the dot product)
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-        qv[h] = *reinterpret_cast<const f16x8*>(q + ((size_t)b * hq + kvh * G + h) * D + li * 8);
+    // q of this head, raw fp16 (scaled after the dot product)
+    const f16x8 qv = *reinterpret_cast<const f16x8*>(q + ((size_t)b * hq + kvh) * D + li * 8);
     const int stride = T::NW * T::TOK;
     int pg[T::U];
     load_pages(start + w * T::TOK, min(start + partition, max_tok), pg);
-    // Fast path (page size 16, a chunk wholly inside the context): the chunk's
-    // PPI page ids are wave-uniform scalar loads, and every K/V load is one
-    // instruction, page base (SGPR) + lane offset + immediate.  Loaded one
-    // chunk ahead like pg; the first chunk's together with pg.  Head groups
-    // only: with one query head per kv head the loop is not issue-bound, and
-    // the checked loads measured 1% faster there (MI355X, same box); with 4 or
-    // 8 heads this path is 4-11% faster.
-    const bool fast_bs = G >= 2 && bs == T::FAST_BS;
-    int spg[T::PPI];
-    auto load_spages = [&](int t0) {
-#pragma unroll
-        for (int p = 0; p < T::PPI; ++p) spg[p] = bt[uniform((t0 >> 4) + p)];
-    };
-    if (fast_bs && start + w * T::TOK + T::TOK <= min(start + partition, max_tok)) load_spages(start + w * T::TOK);
 
     const int ctx = min(ctx_raw, max_tok);
     if (start >= ctx) {  // whole workgroup: this split is past the context
         // A sequence with no context (outside the >= 1 contract) gets a zero row,
         // as the reduce gives it when there are several splits.
         if (num_splits == 1)
-            for (int idx = tid; idx < G * D; idx += T::THREADS)
-                out[((size_t)b * hq + kvh * G + idx / D) * D + idx % D] = (f16)0.f;
+            for (int idx = tid; idx < D; idx += T::THREADS) out[((size_t)b * hq + kvh) * D + idx] = (f16)0.f;
         return;
     }
     const int end = min(ctx, start + partition);
 
-    float m[G], l[G], acc[G][8];
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-        m[h] = -INFINITY;
-        l[h] = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[h][i] = 0.f;
-    }
+    float m[G] = {-INFINITY}, l[G] = {0.f}, acc[G][8] = {};
     const size_t page_stride = (size_t)hkv * bs * D;
     const size_t head_off = (size_t)kvh * bs * D + li * 8;
 
-    // Scores, online softmax and P V of one chunk: kr/vr hold token
-    // t0 + u*TPL + gi of each u; tokens with !valid[u] drop out.
-    auto consume = [&](const f16x8 (&kr)[T::U], const f16x8 (&vr)[T::U], const bool (&valid)[T::U], auto masked) {
-        constexpr bool MASKED = decltype(masked)::value;
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            float s[T::U];
-            float mx = -INFINITY;
-#pragma unroll
-            for (int u = 0; u < T::U; ++u) {
-                const float dsum = group_sum<T::LPT>(dot8(qv[h], kr[u]));
-                s[u] = !MASKED || valid[u] ? dsum * sl2 : -INFINITY;
-                mx = fmaxf(mx, s[u]);
-            }
-            const float m_new = fmaxf(m[h], mx);
-            const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-            const float alpha = exp2_fast(m[h] - m_use);
-            float psum = 0.f;
-#pragma unroll
-            for (int u = 0; u < T::U; ++u) {
-                s[u] = exp2_fast(s[u] - m_use);
-                psum += s[u];
-            }
-            l[h] = l[h] * alpha + psum;
-            m[h] = m_new;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                float a = acc[h][i] * alpha;
-#pragma unroll
-                for (int u = 0; u < T::U; ++u) a = fmaf(s[u], (float)vr[u][i], a);
-                acc[h][i] = a;
-            }
-        }
-    };
-    // Byte offset of this lane's 16 bytes inside a 16-token page of its kv head.
-    const uint32_t lane_off = (uint32_t)(((size_t)kvh * T::FAST_BS * D + gi * D + li * 8) * sizeof(f16));
-
-    // Fast loop: whole chunks of 16-token pages with valid page ids.  Its page
-    // ids are prefetched as spg while the next chunk is also a fast one, else
-    // as pg for the checked loop, which takes the rest (the context's tail,
-    // other page sizes, out-of-range page ids).
-    int t0 = start + w * T::TOK;
-    while (fast_bs && t0 + T::TOK <= end) {
-        bool pages_ok = true;
-#pragma unroll
-        for (int p = 0; p < T::PPI; ++p) pages_ok = pages_ok && (unsigned)spg[p] < (unsigned)num_blocks;
-        if (!pages_ok) {
-            load_pages(t0, end, pg);
-            break;
-        }
-        f16x8 kr[T::U], vr[T::U];
-#pragma unroll
-        for (int u = 0; u < T::U; ++u) {
-            const int p = u * T::TPL / T::FAST_BS, row = u * T::TPL % T::FAST_BS;
-            const size_t pbase = (size_t)spg[p] * page_stride * sizeof(f16);
-            const uint32_t off = lane_off + (uint32_t)(row * D * sizeof(f16));
-            // K/V are streamed once: non-temporal loads keep them out of the caches' way.
-            kr[u] = __builtin_nontemporal_load(
-                reinterpret_cast<const f16x8*>(reinterpret_cast<const char*>(kc) + pbase + off));
-            vr[u] = __builtin_nontemporal_load(
-                reinterpret_cast<const f16x8*>(reinterpret_cast<const char*>(vc) + pbase + off));
-        }
-        const int tn = t0 + stride;
-        if (tn + T::TOK <= end) load_spages(tn);
-        else load_pages(tn, end, pg);
-        const bool unused[T::U] = {};  // unmasked: every token of a whole-page chunk is valid
-        consume(kr, vr, unused, std::false_type{});
-        t0 = tn;
-    }
-    for (; t0 < end; t0 += stride) {
+    // One chunk: token t0 + u*TPL + gi in kr[u]/vr[u]; tokens with !valid[u]
+    // drop out.  Each group of D/8 lanes reduces its dot products with a DPP
+    // tree and runs its own online softmax.
+    for (int t0 = start + w * T::TOK; t0 < end; t0 += stride) {
         f16x8 kr[T::U], vr[T::U];
         bool valid[T::U];
 #pragma unroll
@@ -230,11 +124,37 @@ paged_decode_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const
             const bool ok = t < end && (unsigned)pg[u] < (unsigned)num_blocks;  // bad page ids are never read
             const size_t off = (size_t)(ok ? pg[u] : 0) * page_stride + head_off + (size_t)po * D;
             valid[u] = ok;
+            // K/V are streamed once: non-temporal loads keep them out of the caches' way.
             kr[u] = ok ? __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(kc + off)) : f16x8{};
             vr[u] = ok ? __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(vc + off)) : f16x8{};
         }
         load_pages(t0 + stride, end, pg);
-        consume(kr, vr, valid, std::true_type{});
+        float sc[T::U];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < T::U; ++u) {
+            const float dsum = group_sum<T::LPT>(dot8(qv, kr[u]));
+            sc[u] = valid[u] ? dsum * sl2 : -INFINITY;
+            mx = fmaxf(mx, sc[u]);
+        }
+        const float m_new = fmaxf(m[0], mx);
+        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+        const float alpha = exp2_fast(m[0] - m_use);
+        float psum = 0.f;
+#pragma unroll
+        for (int u = 0; u < T::U; ++u) {
+            sc[u] = exp2_fast(sc[u] - m_use);
+            psum += sc[u];
+        }
+        l[0] = l[0] * alpha + psum;
+        m[0] = m_new;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float a = acc[0][i] * alpha;
+#pragma unroll
+            for (int u = 0; u < T::U; ++u) a = fmaf(sc[u], (float)vr[u][i], a);
+            acc[0][i] = a;
+        }
     }
 
     // Merge the token groups of the wave (lanes that share li), then the waves.
@@ -291,6 +211,405 @@ paged_decode_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const
             if (d == 0) {
                 m_part[row * num_splits + split] = M;
                 l_part[row * num_splits + split] = L;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Grouped-query decode: G = 2, 4 or 8 query heads per kv head.
+//
+// The kernel above, given head groups, runs out of VALU issue before HBM: each
+// (head, token) dot product is reduced over its D/8 lanes by a DPP tree, every
+// lane of the group then exponentiates the same score, and P V converts V to
+// fp32 and spends one FMA per (head, token, dim).  This kernel reads the cache
+// exactly as that one does (D/8 lanes per token row, one 16-byte K and V load
+// per lane per token, scalar page ids, one 16-token page per wave chunk) and
+// reorganises the arithmetic of a chunk:
+//   * reduce-scatter: a lane's G*U partial dot products (8 dims each) are
+//     summed across its lane group by a butterfly that halves the list at
+//     every lane bit: the lane keeps one half and adds the partner's copy of it
+//     (DPP), so the G*U sums cost about G*U DPP adds instead of log2(D/8) * G*U,
+//     and every lane ends with the full scores of one head and two tokens.  So
+//     that each step is one DPP add with no selects, a lane holds its q heads
+//     and its token slots in a lane-dependent order: register r holds value
+//     r ^ f(lane), where f toggles the bit resolved at each butterfly stage;
+//   * every score is exponentiated once, against a per-wave, per-head reference
+//     max m that moves only when a score exceeds it by more than 8 (base 2), so
+//     that P = 2^(s - m + 7) stays below 2^15 and is exact enough in fp16 (the
+//     2^7 keeps small weights out of fp16's subnormal range; it cancels in o/l);
+//   * P goes to fp16, two tokens per register, and is all-gathered across the
+//     lane group by the inverse butterfly; P V is v_dot2_f32_f16 over token
+//     pairs (V repacked pairwise with v_perm), into fp32 accumulators; l sums
+//     the same fp16 P values, so rounding P only perturbs the weights.
+// Lanes of one group hold the same head order, so the groups of a wave merge
+// register by register at the end (lane permutes, no LDS), and the waves of the
+// workgroup through LDS as above.
+
+template <int D, int G>
+struct GqaTile {
+    static constexpr int NW = 4;                 // waves per workgroup
+    static constexpr int THREADS = NW * kWave;
+    static constexpr int LPT = D / 8;            // lanes per token row (a lane group)
+    static constexpr int TPL = kWave / LPT;      // tokens per wave-wide load
+    static constexpr int U = 16 / TPL;           // K (and V) loads per lane per chunk
+    static constexpr int TOK = U * TPL;          // tokens per wave chunk: one 16-token page
+    static constexpr int LB = D == 128 ? 4 : 3;  // log2(LPT): butterfly stages of a lane group
+    static constexpr int N = G * U;              // partial dot products per lane per chunk
+    static constexpr int LOGN = G * U == 4 ? 2 : G * U == 8 ? 3 : G * U == 16 ? 4 : 5;
+    static constexpr int S = LB < LOGN - 1 ? LB : LOGN - 1;  // stages that scatter
+    static constexpr int HB = G == 2 ? 1 : G == 4 ? 2 : 3;   // head bits of a value index
+    static_assert(D == 128 || D == 64, "head dim");
+    static_assert(G == 2 || G == 4 || G == 8, "head group");
+    static_assert((N >> S) == 2, "two scores per lane after the scatter");
+    static_assert(S >= HB, "the scatter resolves every head bit");
+};
+
+// The butterfly's partner at stage s is lane ^ mask(s) inside the lane group.
+// 16-lane groups: masks 8, 7, 2, 1 (DPP row_ror:8, row_half_mirror, quad_perm
+// [2,3,0,1], quad_perm [1,0,3,2]); 8-lane groups: 7, 2, 1.  They are linearly
+// independent over GF(2), so every lane has unique coordinates c_s in them.
+template <int LB>
+__device__ constexpr int bfly_dpp(int s) {
+    constexpr int k16[4] = {0x128, kDppHalfMirror, kDppXor2, kDppXor1};
+    return k16[s + 4 - LB];
+}
+template <int LB>
+__device__ __forceinline__ int bfly_coord(int li, int s) {
+    // li = XOR_s c_s * mask(s) with masks (8,) 7, 2, 1: bit 3 only in 8, bit 2
+    // only in 7, bit 1 in 7 and 2, bit 0 in 7 and 1.
+    const int l2 = (li >> 2) & 1;
+    const int c[4] = {(li >> 3) & 1, l2, ((li >> 1) & 1) ^ l2, (li & 1) ^ l2};
+    return c[s + 4 - LB];
+}
+
+// Lane mask, inside a lane group, from a lane holding head h to a lane that
+// holds head h ^ a: the masks of the stages that resolve the head bits set in a.
+template <int LB, int N, int G>
+__device__ constexpr int head_lane_mask(int a) {
+    constexpr int k16[4] = {8, 7, 2, 1};
+    int m = 0;
+    for (int s = 0; s < LB && (N >> (s + 1)) >= 2; ++s) {
+        const int bit = N >> (s + 1);  // value-index bit resolved at stage s
+        if (bit < 2 * G && (a & (bit >> 1))) m ^= k16[s + 4 - LB];
+    }
+    return m;
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, false);
+}
+
+template <int I, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < E) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, E>(f);
+    }
+}
+
+// x combined by op with the value of lane l ^ MASK (MASK = 8, 16 or 32): DPP
+// row_ror:8, or v_permlane16/32_swap on two copies of x (inline asm, as in the
+// prefill kernel: the builtin with identical inputs kept one register).  The
+// s_nop covers the VALU-write -> permlane-read hazard.
+template <int MASK, class Op>
+__device__ __forceinline__ float xor_combine(float x, Op op) {
+    static_assert(MASK == 8 || MASK == 16 || MASK == 32, "lane mask");
+    if constexpr (MASK == 8) {
+        return op(x, dpp<0x128>(x));
+    } else {
+        float a = x, b = x;
+        if constexpr (MASK == 16)
+            asm volatile("s_nop 2\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+        else
+            asm volatile("s_nop 2\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+        return op(a, b);
+    }
+}
+// x combined over the TPL lane groups of the wave (lanes l ^ LPT, l ^ 2 LPT, ...).
+template <int LPT, class Op>
+__device__ __forceinline__ float across_groups(float x, Op op) {
+    if constexpr (LPT == 8) x = xor_combine<8>(x, op);
+    x = xor_combine<16>(x, op);
+    return xor_combine<32>(x, op);
+}
+
+template <int D, int G>
+__global__ void __launch_bounds__((GqaTile<D, G>::THREADS))
+paged_decode_gqa_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const f16* __restrict__ vc,
+                        const int* __restrict__ block_tables, const int* __restrict__ ctx_lens,
+                        f16* __restrict__ out, float* __restrict__ o_part, float* __restrict__ m_part,
+                        float* __restrict__ l_part, int hkv, int bs, int bs_shift, int max_blocks,
+                        int num_blocks, int partition, int num_splits, float sl2) {
+    using T = GqaTile<D, G>;
+    constexpr int U = T::U, N = T::N, S = T::S, LB = T::LB;
+    // P = 2^(s - m + kPShift): the largest P the fast path accepts is 2^kPMax.
+    constexpr float kPShift = 7.f, kPMax = 32768.f;
+    __shared__ float red_acc[T::NW][G][D];
+    __shared__ float red_m[T::NW][G], red_l[T::NW][G];
+
+    const int kvh = blockIdx.x, split = blockIdx.y, b = blockIdx.z;
+    const int hq = hkv * G;
+    const int start = split * partition;
+    const int tid = threadIdx.x, lane = tid & 63, w = uniform(tid >> 6);
+    const int gi = lane / T::LPT, li = lane % T::LPT;
+    const int* bt = block_tables + (size_t)b * max_blocks;
+    const int max_tok = max_blocks * bs;
+
+    // Value index of a partial dot product: j = (slot >> 1) * 2G + head * 2 +
+    // (slot & 1).  Stage s of the butterfly resolves bit N >> (s + 1), top
+    // first, so a slot's high bit (if U = 4) is resolved by the first stage,
+    // whose partner mask 8 is the cache-line bit of the lane (lanes 0-7 and
+    // 8-15 read the two 128-byte halves of a 256-byte row): the 8 lanes of a
+    // cache line always read the same token row, and every load instruction
+    // reads whole lines.  This lane's offset f into the value index:
+    int f = 0;
+#pragma unroll
+    for (int s = 0; s < S; ++s) f ^= bfly_coord<LB>(li, s) ? (N >> (s + 1)) : 0;
+    constexpr int LG = G == 2 ? 1 : G == 4 ? 2 : 3;
+    auto head_of = [](int j) { return (j >> 1) & (G - 1); };
+    auto slot_of = [](int j) { return ((j >> (1 + LG)) << 1) | (j & 1); };
+    const int fh = head_of(f), fu = slot_of(f);
+
+    // Page ids of this lane's token slots (slot u holds token t0 + (u ^ fu) *
+    // TPL + gi) below lim, -1 elsewhere; loaded one chunk ahead.
+    auto load_pages = [&](int t0, int lim, int (&pg)[U]) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int t = t0 + (u ^ fu) * T::TPL + gi;
+            const int pi = bs_shift >= 0 ? (t >> bs_shift) : (t / bs);
+            pg[u] = t < lim ? bt[pi] : -1;
+        }
+    };
+    const int ctx_raw = ctx_lens[b];
+    f16x8 qv[G];  // register a: query head a ^ fh
+#pragma unroll
+    for (int a = 0; a < G; ++a)
+        qv[a] = *reinterpret_cast<const f16x8*>(q + ((size_t)b * hq + kvh * G + (a ^ fh)) * D + li * 8);
+    const int stride = T::NW * T::TOK;
+    int pg[U];
+    const bool fast_bs = bs == T::TOK;
+    int spg = 0;
+    if (fast_bs && start + w * T::TOK + T::TOK <= min(start + partition, max_tok))
+        spg = bt[uniform((start + w * T::TOK) >> 4)];
+
+    const int ctx = min(ctx_raw, max_tok);
+    if (start >= ctx) {
+        if (num_splits == 1)
+            for (int idx = tid; idx < G * D; idx += T::THREADS)
+                out[((size_t)b * hq + kvh * G + idx / D) * D + idx % D] = (f16)0.f;
+        return;
+    }
+    const int end = min(ctx, start + partition);
+
+    // Per-wave reference max of this lane's head (fh), this lane's share of l
+    // for that head, and the accumulators (register a: head a ^ fh, dims
+    // li*8 .. li*8+7, this lane group's tokens).
+    float m_own = -INFINITY, l_own = 0.f;
+    float acc[G][8];
+#pragma unroll
+    for (int a = 0; a < G; ++a)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[a][i] = 0.f;
+    const size_t page_stride = (size_t)hkv * bs * D;
+    const size_t head_off = (size_t)kvh * bs * D + li * 8;
+
+    // Scores of a chunk: the full dot products of head fh with this lane's own
+    // slots 0 and 1 (after which the K registers are free).
+    auto scores = [&](const f16x8 (&kr)[U], float (&xs)[2]) {
+        // Partial dot products: x[r] = q(head head_of(r) ^ fh) . k(slot slot_of(r) ^ fu), 8 dims.
+        float x[N];
+#pragma unroll
+        for (int r = 0; r < N; ++r) x[r] = dot8(qv[head_of(r)], kr[slot_of(r)]);
+        // Reduce-scatter over the lane group; the remaining stages (lane bits
+        // left after every head bit and every slot bit but the lowest is
+        // resolved) sum the two remaining values in full.
+        static_for<0, S>([&](auto st) {
+            constexpr int s = decltype(st)::value, half = (N >> s) / 2;
+#pragma unroll
+            for (int r = 0; r < half; ++r) x[r] += dpp<bfly_dpp<LB>(s)>(x[r + half]);
+        });
+        static_for<S, LB>([&](auto st) {
+            constexpr int s = decltype(st)::value;
+            x[0] += dpp<bfly_dpp<LB>(s)>(x[0]);
+            x[1] += dpp<bfly_dpp<LB>(s)>(x[1]);
+        });
+        xs[0] = x[0];
+        xs[1] = x[1];
+    };
+    // Online softmax and P V of a chunk, from its scores and its V registers;
+    // tokens with !valid[r] (this lane's slots 0 and 1) drop out when MASKED.
+    auto finish = [&](const float (&x)[2], const f16x8 (&vr)[U], const bool (&valid)[U], auto masked) {
+        constexpr bool MASKED = decltype(masked)::value;
+        float p[2];
+        float bias = kPShift - m_own;
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+            p[r] = exp2_fast(!MASKED || valid[r] ? fmaf(x[r], sl2, bias) : -INFINITY);
+        const bool ok = p[0] <= kPMax && p[1] <= kPMax;  // false for inf and NaN
+        if (__builtin_amdgcn_ballot_w64(!ok)) {
+            // Move the reference max of every head of the wave to its running
+            // max (first chunk: m = -inf; later: a score above m + 8).
+            float mx = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 2; ++r) mx = fmaxf(mx, !MASKED || valid[r] ? x[r] * sl2 : -INFINITY);
+            auto fmax2 = [](float u, float v) { return fmaxf(u, v); };
+            static_for<0, LB>([&](auto st) {
+                constexpr int s = decltype(st)::value;
+                if constexpr (s >= S || (N >> (s + 1)) >= 2 * G) mx = fmaxf(mx, dpp<bfly_dpp<LB>(s)>(mx));
+            });
+            mx = across_groups<T::LPT>(mx, fmax2);
+            const float m_new = fmaxf(m_own, mx);
+            const float m_use = m_new == -INFINITY ? 0.f : m_new;
+            const float alpha = exp2_fast(m_own - m_use);  // 0 while m was -inf
+            l_own *= alpha;
+            m_own = m_new;
+            // Every lane of head fh holds the same alpha; the accumulators of
+            // head a ^ fh take theirs from the lane of the group that holds
+            // that head (a lane shuffle: no memory, nothing to order).
+            static_for<0, G>([&](auto ai) {
+                constexpr int a = decltype(ai)::value;
+                const float al = a == 0 ? alpha : __shfl_xor(alpha, head_lane_mask<LB, N, G>(a), kWave);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[a][i] *= al;
+            });
+            bias = kPShift - m_use;
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+                p[r] = exp2_fast(!MASKED || valid[r] ? fmaf(x[r], sl2, bias) : -INFINITY);
+        }
+        const f16x2 pp = {(f16)p[0], (f16)p[1]};
+        l_own = __builtin_amdgcn_fdot2(pp, f16x2{(f16)1.f, (f16)1.f}, l_own, false);
+        // All-gather P over the lane group (the scatter's stages in reverse):
+        // register k = pr * G + a then holds the pair of head a ^ fh, slots
+        // (2 pr) ^ fu and +1, i.e. the tokens in V registers 2 pr and 2 pr + 1.
+        uint32_t P[N / 2];
+        P[0] = __builtin_bit_cast(uint32_t, pp);
+        static_for<0, S>([&](auto st) {
+            constexpr int s = S - 1 - decltype(st)::value, m = N >> (s + 2);
+#pragma unroll
+            for (int k = 0; k < m; ++k) P[k + m] = dpp_u32<bfly_dpp<LB>(s)>(P[k]);
+        });
+        // P V over token pairs: vp[i] = (v(slot 2pr)[i], v(slot 2pr+1)[i]).
+#pragma unroll
+        for (int pr = 0; pr < U / 2; ++pr) {
+            const auto lo = __builtin_bit_cast(u32x4, vr[2 * pr]);
+            const auto hi = __builtin_bit_cast(u32x4, vr[2 * pr + 1]);
+            f16x2 vp[8];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                vp[2 * k] = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(hi[k], lo[k], 0x05040100u));
+                vp[2 * k + 1] = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(hi[k], lo[k], 0x07060302u));
+            }
+#pragma unroll
+            for (int a = 0; a < G; ++a) {
+                const f16x2 pa = __builtin_bit_cast(f16x2, P[pr * G + a]);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[a][i] = __builtin_amdgcn_fdot2(pa, vp[i], acc[a][i], false);
+            }
+        }
+    };
+    // Byte offset of slot u's 16 bytes inside a 16-token page of this kv head.
+    uint32_t lane_off[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        lane_off[u] = (uint32_t)(((size_t)kvh * T::TOK * D + ((u ^ fu) * T::TPL + gi) * D + li * 8) * sizeof(f16));
+
+    // Whole-page chunks: the chunk's page id is one wave-uniform scalar load
+    // (prefetched one chunk ahead) and every K/V load is page base + lane
+    // offset.  The checked loop takes the rest: the context's tail, an
+    // out-of-range page id, and every chunk when pages are not 16 tokens.
+    // (Software-pipelining this loop, the next chunk's K and V issued under
+    // this chunk's work, measured 0-7% slower on MI355X: the loop is not
+    // latency-bound at 3-4 waves per SIMD.)
+    int t0 = start + w * T::TOK;
+    {
+        auto load_kv = [&](const f16* cache, int pid, f16x8 (&r)[U]) {
+            const char* base = reinterpret_cast<const char*>(cache) + (size_t)pid * page_stride * sizeof(f16);
+#pragma unroll
+            for (int u = 0; u < U; ++u)  // streamed once: non-temporal
+                r[u] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(base + lane_off[u]));
+        };
+        const bool unused[U] = {};
+        while (fast_bs && t0 + T::TOK <= end && (unsigned)spg < (unsigned)num_blocks) {
+            f16x8 kr[U], vr[U];
+            load_kv(kc, spg, kr);
+            load_kv(vc, spg, vr);
+            const int tn = t0 + stride;
+            if (tn + T::TOK <= end) spg = bt[uniform(tn >> 4)];
+            float x[2];
+            scores(kr, x);
+            finish(x, vr, unused, std::false_type{});
+            t0 = tn;
+        }
+    }
+    if (t0 < end) load_pages(t0, end, pg);
+    for (; t0 < end; t0 += stride) {
+        f16x8 kr[U], vr[U];
+        bool valid[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int t = t0 + (u ^ fu) * T::TPL + gi;
+            const int po = bs_shift >= 0 ? (t & (bs - 1)) : (t % bs);
+            const bool ok = t < end && (unsigned)pg[u] < (unsigned)num_blocks;
+            const size_t off = (size_t)(ok ? pg[u] : 0) * page_stride + head_off + (size_t)po * D;
+            valid[u] = ok;
+            kr[u] = ok ? __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(kc + off)) : f16x8{};
+            vr[u] = ok ? __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(vc + off)) : f16x8{};
+        }
+        load_pages(t0 + stride, end, pg);
+        float x[2];
+        scores(kr, x);
+        finish(x, vr, valid, std::true_type{});
+    }
+
+    // Merge the wave: l over the lanes of each head (the stages that resolved
+    // slot bits; the plain stages hold copies), then everything over the lane
+    // groups.  m is already per wave and head, so these are plain sums.
+    auto add2 = [](float u, float v) { return u + v; };
+    static_for<0, S>([&](auto st) {
+        constexpr int s = decltype(st)::value;
+        if constexpr ((N >> (s + 1)) >= 2 * G) l_own += dpp<bfly_dpp<LB>(s)>(l_own);
+    });
+    l_own = across_groups<T::LPT>(l_own, add2);
+#pragma unroll
+    for (int a = 0; a < G; ++a)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[a][i] = across_groups<T::LPT>(acc[a][i], add2);
+    if (gi == 0) {
+#pragma unroll
+        for (int a = 0; a < G; ++a)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) red_acc[w][a ^ fh][li * 8 + i] = acc[a][i];
+        red_m[w][fh] = m_own;
+        red_l[w][fh] = l_own;
+    }
+    __syncthreads();
+    for (int idx = tid; idx < G * D; idx += T::THREADS) {
+        const int h = idx / D, d = idx % D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < T::NW; ++v) M = fmaxf(M, red_m[v][h]);
+        const float Mu = M == -INFINITY ? 0.f : M;
+        float L = 0.f, o = 0.f;
+#pragma unroll
+        for (int v = 0; v < T::NW; ++v) {
+            const float wv = exp2_fast(red_m[v][h] - Mu);
+            L += red_l[v][h] * wv;
+            o += red_acc[v][h][d] * wv;
+        }
+        o = L > 0.f ? o / L : 0.f;
+        const size_t row = (size_t)b * hq + kvh * G + h;
+        if (num_splits == 1) {
+            out[row * D + d] = (f16)o;
+        } else {
+            o_part[(row * num_splits + split) * D + d] = o;
+            if (d == 0) {
+                // m in the log2 domain of the scores, as the reduce expects:
+                // the kPShift on P cancels in o and is taken out of l here.
+                m_part[row * num_splits + split] = M;
+                l_part[row * num_splits + split] = L * (1.f / 128.f);
             }
         }
     }
@@ -364,16 +683,22 @@ paged_reduce_kernel(const float* __restrict__ o_part, const float* __restrict__ 
 
 template <int D, int G>
 static hipError_t launch_decode(const DecodeArgs& a) {
-    using T = DecodeTile<D, G>;
     int bs_shift = -1;
     for (int s = 0; s < 31; ++s)
         if ((int64_t(1) << s) == a.bs) bs_shift = s;
     const hipStream_t stream = (hipStream_t)a.stream;
     dim3 grid((unsigned)a.hkv, (unsigned)a.num_splits, (unsigned)a.batch);
-    hipLaunchKernelGGL((paged_decode_kernel<D, G>), grid, dim3(T::THREADS), 0, stream, (const f16*)a.q,
-                       (const f16*)a.k_cache, (const f16*)a.v_cache, a.block_tables, a.context_lens,
-                       (f16*)a.out, a.o_part, a.m_part, a.l_part, (int)a.hkv, (int)a.bs, bs_shift,
-                       (int)a.max_blocks, (int)a.num_blocks, (int)a.partition, (int)a.num_splits, a.sl2);
+    if constexpr (G == 1)
+        hipLaunchKernelGGL((paged_decode_kernel<D>), grid, dim3(DecodeTile<D>::THREADS), 0, stream, (const f16*)a.q,
+                           (const f16*)a.k_cache, (const f16*)a.v_cache, a.block_tables, a.context_lens,
+                           (f16*)a.out, a.o_part, a.m_part, a.l_part, (int)a.hkv, (int)a.bs, bs_shift,
+                           (int)a.max_blocks, (int)a.num_blocks, (int)a.partition, (int)a.num_splits, a.sl2);
+    else
+        hipLaunchKernelGGL((paged_decode_gqa_kernel<D, G>), grid, dim3(GqaTile<D, G>::THREADS), 0, stream,
+                           (const f16*)a.q, (const f16*)a.k_cache, (const f16*)a.v_cache, a.block_tables,
+                           a.context_lens, (f16*)a.out, a.o_part, a.m_part, a.l_part, (int)a.hkv, (int)a.bs,
+                           bs_shift, (int)a.max_blocks, (int)a.num_blocks, (int)a.partition,
+                           (int)a.num_splits, a.sl2);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.num_splits == 1) return e;
     hipLaunchKernelGGL((paged_reduce_kernel<D>), dim3((unsigned)(a.batch * a.hq)), dim3(256), 0, stream,

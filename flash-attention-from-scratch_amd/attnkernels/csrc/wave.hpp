@@ -18,6 +18,7 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // log2(e): softmax runs in base 2, exp(x) = 2^(x * log2 e), with the softmax
 // scale folded into the same multiply (the reference's convention, README.md:80-82).

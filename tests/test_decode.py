@@ -67,8 +67,9 @@ CHUNK_EDGES = [15, 16, 17, 31, 32, 33, 63, 65, 127, 129, 255, 257, 383, 385, 511
 @pytest.mark.parametrize("partition", [256, 512])
 def test_chunk_edges_head_groups(d, hq, hkv, partition):
     """Context lengths one token either side of every chunk size the head-group
-    tiles use: 16, 32 or 64 tokens per wave, 64 to 256 per workgroup step; the
-    whole-page loop hands the tail to the checked loop at each of them."""
+    kernel uses (16 tokens, one page, per wave; 64 per workgroup step) and of
+    the splits; the whole-page loop hands the tail to the checked loop at each
+    of them."""
     assert run(CHUNK_EDGES, hq, hkv, d, partition=partition) < TOL[d]
 
 
@@ -328,3 +329,29 @@ def test_empty_context_gives_zero_rows(partition):
     for b in (1, 3):
         ref = oracle.paged_decode_fp32(q[b:b + 1], kc, vc, bt[b:b + 1], cl[b:b + 1])
         assert max_err(out[b:b + 1], ref) < TOL[128], b
+
+
+@pytest.mark.parametrize("d,hq,hkv", [(128, 8, 4), (128, 32, 8), (128, 16, 2), (64, 32, 8), (64, 16, 2)])
+def test_head_groups_repeatable_after_other_kernels(d, hq, hkv):
+    """The grouped-query kernel exchanges values between lanes only through lane
+    permutes; nothing it reads depends on what earlier kernels left in LDS or in
+    the workspace.  Twelve calls, each after a prefill launch that fills LDS with
+    other data, must give the same bits, all finite."""
+    lens = [5000, 1, 700]
+    kc, vc, bt, cl = cache(lens, hkv, d, seed=71)
+    q = rand_q(len(lens), hq, d, seed=72)
+    args = to_dev(q, kc, vc, bt, cl)
+    g = torch.Generator(device="cuda").manual_seed(73)
+    x = torch.randn(2, 8, 1024, d, generator=g, device="cuda", dtype=torch.float16) * 1e4
+    first = None
+    for i in range(12):
+        ak.flash_attention(x, x, x, causal=bool(i % 2))
+        out = ak.paged_decode(*args, max(lens), partition_size=256 if i % 3 else None)
+        torch.cuda.synchronize()
+        assert torch.isfinite(out).all(), i
+        if first is None:
+            first = out.clone()
+            ref = oracle.paged_decode_fp32(q, kc, vc, bt, cl)
+            assert max_err(out, ref) < TOL[d]
+        elif i % 3:
+            assert torch.equal(out, first) or max_err(out, ref) < TOL[d], i
