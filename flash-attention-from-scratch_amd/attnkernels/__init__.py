@@ -102,36 +102,44 @@ def _sm_count(device_index):
     return torch.cuda.get_device_properties(device_index).multi_processor_count
 
 
-# Split-count target of decode_partition, in decode workgroups per compute
-# unit.  The reference's rule aims at 4 blocks per SM (attnkernels/__init__.py:
-# 94-98, tuned on a T4).  The partition is chosen from max_context_len alone
-# (reading the lengths would cost a host sync), so the rule must hold for
-# uniform and for mixed-length batches.  The MI355X split-K ablation of
-# ``attnkernels.benchsuite`` (every power-of-two partition; 5 uniform and 3
-# mixed-length batches, Hkv=8, results/mi355x.md) sets both constants:
-#   * 16 workgroups per CU: with fewer, the longest sequences of a mixed batch
-#     are left as a tail (the reference's 4 reaches only 78% of the best
-#     partition there);
-#   * at least 2 chunks (512 tokens) per split: a 256-token split pays a
-#     workgroup's fixed costs (page ids, then K/V, before any work; the merge)
-#     for little work.
-# Together they reach >= 88% of the best partition in every case (mean 96%);
-# with 1-chunk splits the worst case is 85%.
-DECODE_WG_PER_CU = 16
-DECODE_MIN_CHUNKS = 2
+# Split-count target of decode_partition.  The reference's rule aims at 4
+# blocks per SM (attnkernels/__init__.py:94-98, tuned on a T4).  The partition
+# is chosen from max_context_len alone (reading the lengths would cost a host
+# sync), so the rule must hold for uniform and for mixed-length batches.  The
+# MI355X split-K ablation of ``attnkernels.benchsuite`` (every power-of-two
+# partition; 12 uniform and 5 mixed-length batches over one, four and eight
+# query heads per kv head; results/mi355x.md) sets the three constants:
+#   * 8 workgroups per CU: uniform batches run fastest with few, long splits
+#     (256-512 workgroups in all), mixed batches with more (their short
+#     sequences leave most nominal splits empty);
+#   * at least 4 chunks (1024 tokens) per split where the context has them: a
+#     short split pays a workgroup's fixed costs (page ids, q, then K/V before
+#     any work; the merge; a partial for the reduce) for little work;
+#   * no split once B * Hkv reaches 2 workgroups per CU: the batch alone fills
+#     the GPU, and the reduce would only add a launch.
+# Together they reach 98% of the best partition on average, >= 87% in every
+# case (the old 16 per CU with 2-chunk splits: 95% and 82%).
+DECODE_WG_PER_CU = 8
+DECODE_MIN_CHUNKS = 4
+DECODE_NO_SPLIT_BLOCKS_PER_CU = 2
 REFERENCE_WG_PER_SM = 4
 
 
 def decode_partition(batch, num_kv_heads, max_context_len, device=None, wg_per_cu=DECODE_WG_PER_CU,
-                     min_chunks=DECODE_MIN_CHUNKS):
+                     min_chunks=DECODE_MIN_CHUNKS, no_split_blocks_per_cu=DECODE_NO_SPLIT_BLOCKS_PER_CU):
     """Tokens per split for paged_decode: enough splits for about ``wg_per_cu``
     workgroups per CU in total, at least ``min_chunks`` 256-token chunks per
-    split where the context has them (reference attnkernels/__init__.py:93-101,
-    whose rule is ``wg_per_cu=REFERENCE_WG_PER_SM, min_chunks=1``)."""
+    split where the context has them, and one split once ``batch *
+    num_kv_heads`` reaches ``no_split_blocks_per_cu`` per CU (reference
+    attnkernels/__init__.py:93-101, whose rule is ``wg_per_cu=REFERENCE_WG_PER_SM,
+    min_chunks=1, no_split_blocks_per_cu=None``)."""
     dev = torch.cuda.current_device() if device is None else device
     blocks = batch * num_kv_heads
-    want = -(-int(wg_per_cu) * _sm_count(dev) // blocks)
+    cus = _sm_count(dev)
     max_chunks = -(-max_context_len // CHUNK)
+    if no_split_blocks_per_cu is not None and blocks >= no_split_blocks_per_cu * cus:
+        return max(1, max_chunks) * CHUNK
+    want = -(-int(wg_per_cu) * cus // blocks)
     splits = max(1, min(want, -(-max_chunks // int(min_chunks))))
     return -(-max_chunks // splits) * CHUNK
 

@@ -245,17 +245,37 @@ def mixed_lengths(batch, lo, hi, seed):
     return torch.randint(lo, hi + 1, (batch,), generator=torch.Generator().manual_seed(seed)).tolist()
 
 
+# Head shapes of the split-K ablation: (query heads, kv heads).  The layer above
+# (4 query heads per kv head), one query head per kv head (the BASELINE decode
+# configs) and 8 per kv head: each runs a different decode kernel.
+ABLATION_HEADS = ((32, 8), (32, 32), (64, 8))
+
+
 def ablation_builders(quick, status, max_kv_gb):
-    uniform = ((1, 8192),) if quick else ((1, 32768), (4, 8192), (16, 4096), (16, 8192), (64, 1024), (64, 4096))
-    for B, c in uniform:
-        for p in partitions_up_to(c):
-            yield lambda B=B, c=c, p=p: decode_case("split_ablation", [c] * B, ("paged_split",), status, partition=p)
-    mixed = ((8, 512, 8192, 3),) if quick else ((4, 512, 32768, 1), (16, 512, 32768, 2), (64, 1, 4096, 3))
-    for B, lo, hi, seed in mixed:
-        lens = mixed_lengths(B, lo, hi, seed)
-        for p in partitions_up_to(max(lens)):
-            yield lambda lens=lens, p=p: decode_case("split_ablation_ragged", lens, ("paged_split",), status,
-                                                     partition=p, extra=dict(ctx_lens=lens))
+    uniform = {(32, 8): ((1, 32768), (4, 8192), (16, 4096), (16, 8192), (64, 1024), (64, 4096)),
+               (32, 32): ((8, 32768), (16, 8192), (64, 4096)),
+               (64, 8): ((1, 32768), (8, 8192), (64, 4096))}
+    mixed = {(32, 8): ((4, 512, 32768, 1), (16, 512, 32768, 2), (64, 1, 4096, 3)),
+             (32, 32): ((64, 1, 4096, 4),),
+             (64, 8): ((16, 512, 32768, 5),)}
+    if quick:
+        uniform, mixed = {(32, 8): ((1, 8192),)}, {(32, 8): ((8, 512, 8192, 3),)}
+    for (hq, hkv), shapes in uniform.items():
+        for B, c in shapes:
+            if kv_gb([c] * B, hkv) > max_kv_gb:
+                continue
+            for p in partitions_up_to(c):
+                yield lambda B=B, c=c, p=p, hq=hq, hkv=hkv: decode_case("split_ablation", [c] * B, ("paged_split",),
+                                                                        status, partition=p, hq=hq, hkv=hkv)
+    for (hq, hkv), shapes in mixed.items():
+        for B, lo, hi, seed in shapes:
+            lens = mixed_lengths(B, lo, hi, seed)
+            if kv_gb(lens, hkv) > max_kv_gb:
+                continue
+            for p in partitions_up_to(max(lens)):
+                yield lambda lens=lens, p=p, hq=hq, hkv=hkv: decode_case(
+                    "split_ablation_ragged", lens, ("paged_split",), status, partition=p, hq=hq, hkv=hkv,
+                    extra=dict(ctx_lens=lens))
 
 
 def ragged_builders(quick, status, max_kv_gb):

@@ -142,13 +142,13 @@ def ablation_table(rows, section="split_ablation"):
         return ""
     by_case = defaultdict(list)
     for r in sel:
-        by_case[(r["batch"], r["ctx"])].append(r)
+        by_case[(r.get("heads", 32), r.get("kv_heads", 8), r["batch"], r["ctx"])].append(r)
     body = []
-    for (b, c), rs in sorted(by_case.items()):
+    for (hq, hkv, b, c), rs in sorted(by_case.items()):
         best = max(rs, key=lambda r: r["gbs"])
         curve = ", ".join(f"{r['partition']}:{r['gbs']:.0f}" for r in sorted(rs, key=lambda r: r["partition"]))
-        body.append([b, c, best["partition"], f"{best['gbs']:.0f}", curve])
-    return _table(["B", "ctx", "best P", "best GB/s", "P:GB/s"], body)
+        body.append([f"{hq}/{hkv}", b, c, best["partition"], f"{best['gbs']:.0f}", curve])
+    return _table(["Hq/Hkv", "B", "ctx", "best P", "best GB/s", "P:GB/s"], body)
 
 
 def render(data):

@@ -36,7 +36,7 @@ def test_render_synthetic():
     md = report.render(dict(meta=meta, results=_rows()))
     assert "## Prefill" in md and "## Paged decode" in md and "## Split-K partition ablation" in md
     assert "| 2x8192 | 2200.0 | 1100.0 | 88.0% | 2.0x | 5.0e-04 |" in md
-    assert "| 1 | 4096 | 512 | 3600 |" in md  # best partition of the ablation
+    assert "| 32/8 | 1 | 4096 | 512 | 3600 |" in md  # best partition of the ablation
     assert "| 4 | 4096 | 4000 | 800 | 50.0% | 512 | 5.0x |" in md
     assert "50% of 8 TB/s" in md and "50% of 2.5 PFLOP/s" in md
     # peak memory (non-causal only), time per call, head groups, worst error per implementation
