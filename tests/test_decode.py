@@ -262,6 +262,28 @@ def _check_rows(out, q, kcd, vcd, bt, cl, rows, d):
         assert max_err(out[b:b + 1], ref) < TOL[d], b
 
 
+def _gpu_fp32_rows_err(out, qd, kcd, vcd, bt, cl, rows):
+    """Max error of the given output rows against attention computed in float32
+    on the GPU (pages gathered through the table, contiguous bmm operands):
+    covers every row at full size, where the CPU oracle takes one sequence at a
+    time; the oracle remains the checker on the sampled rows."""
+    hkv, bs, d = kcd.shape[1], kcd.shape[2], kcd.shape[3]
+    hq = qd.shape[1]
+    worst = 0.0
+    for b in rows:
+        c = int(cl[b])
+        nb = -(-c // bs)
+        pages = torch.from_numpy(bt[b, :nb]).long().cuda()
+        k = kcd[pages].permute(1, 0, 2, 3).reshape(hkv, nb * bs, d)[:, :c].float()
+        v = vcd[pages].permute(1, 0, 2, 3).reshape(hkv, nb * bs, d)[:, :c].float().contiguous()
+        q = qd[b].float().reshape(hkv, hq // hkv, d)
+        s = torch.bmm(q, k.transpose(1, 2).contiguous()) * d ** -0.5
+        ref = torch.bmm(torch.softmax(s, dim=-1), v).reshape(hq, d)
+        worst = max(worst, (out[b].float() - ref).abs().max().item())
+        del k, v, s
+    return worst
+
+
 def test_baseline_cfg4_ragged_64seqs():
     rng = np.random.default_rng(4)
     lens = rng.integers(1, 4097, size=64).tolist()
@@ -272,6 +294,7 @@ def test_baseline_cfg4_ragged_64seqs():
     torch.cuda.synchronize()
     assert torch.isfinite(out).all()
     _check_rows(out, q, kcd, vcd, bt, cl, list(range(0, 64, 4)) + [63], 128)
+    assert _gpu_fp32_rows_err(out, qd, kcd, vcd, bt, cl, range(64)) < TOL[128]
 
 
 @pytest.mark.parametrize("d", [128, 64])
@@ -283,6 +306,7 @@ def test_baseline_cfg5_long_context(d):
     out = ak.paged_decode(qd, kcd, vcd, btd, cld, 32768, partition_size=256)
     torch.cuda.synchronize()
     _check_rows(out, q, kcd, vcd, bt, cl, [0, 7], d)
+    assert _gpu_fp32_rows_err(out, qd, kcd, vcd, bt, cl, range(8)) < TOL[d]
     # every row: the 128-way split merge agrees with the unsplit kernel
     whole = ak.paged_decode(qd, kcd, vcd, btd, cld, 32768, partition_size=1 << 20)
     assert max_err(out, whole) < TOL[d]
@@ -355,3 +379,19 @@ def test_head_groups_repeatable_after_other_kernels(d, hq, hkv):
             assert max_err(out, ref) < TOL[d]
         elif i % 3:
             assert torch.equal(out, first) or max_err(out, ref) < TOL[d], i
+
+
+@pytest.mark.parametrize("hq,d", [(32, 128), (64, 128), (32, 64)])
+def test_grouped_query_layer_every_row(hq, d):
+    """The bench's grouped-query decode layers (16 x 8192 tokens, 8 kv heads,
+    4 or 8 query heads per kv head) at the default partition: every row against
+    float32 attention on the GPU, sequence 0 against the oracle."""
+    lens = [8192] * 16
+    kcd, vcd, bt, cl = baseline_cache(lens, 8, d, 16, seed=81)
+    q = rand_q(16, hq, d, seed=82)
+    qd, btd, cld = to_dev(q, bt, cl)
+    out = ak.paged_decode(qd, kcd, vcd, btd, cld, 8192)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    _check_rows(out, q, kcd, vcd, bt, cl, [0], d)
+    assert _gpu_fp32_rows_err(out, qd, kcd, vcd, bt, cl, range(16)) < TOL[d]
