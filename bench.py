@@ -12,9 +12,10 @@ idle state), then W untimed warmup steps, then the K timed steps.
 The same line carries, under ``workloads``, the other BASELINE configs measured
 the same way: non-causal prefill, the N=8191 variant, the two
 paged split-K decode configs in KV GB/s with the reference's byte convention
-sum(ctx)*Hkv*D*2*2 (bench/bench.py:199-200), a grouped-query decode layer (4
-query heads per kv head) at the library's default partition, the paged cache
-writer (K/V rows read + written, GB/s), and a packed variable-length GQA prefill.
+sum(ctx)*Hkv*D*2*2 (bench/bench.py:199-200), two grouped-query decode layers (4
+and 8 query heads per kv head) at the library's default partition, the paged
+cache writer (K/V rows read + written, GB/s), and a packed variable-length GQA
+prefill.
 
 ``roofline`` is the headline kernel's algorithmic FLOP per launch divided by its
 mean launch duration (HIP events on the launch stream, inside the timed
