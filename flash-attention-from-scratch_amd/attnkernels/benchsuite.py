@@ -30,6 +30,8 @@ Sections (the row schema ``attnkernels.report`` reads):
                          split, uniform batches
   split_ablation_ragged  the same over batches of mixed context lengths
   ragged                 one mixed-length batch, all decode implementations
+  input_activity         the headline prefill shapes and an 8192^3 fp16 GEMM on
+                         random, random-sign, all-ones and all-zero inputs
 
 SDPA is pinned to its fused backends; its math backend (batched products on
 transposed views, which have faulted GPUs on this pool) never runs.
@@ -288,8 +290,60 @@ def ragged_builders(quick, status, max_kv_gb):
     yield lambda: decode_case("ragged", lens, names, status, extra=dict(ctx_lens=lens))
 
 
+# Input patterns ordered by how many bits they switch in the matrix core:
+# normal random values, random signs of one magnitude, all ones, all zeros.
+ACTIVITY = ("randn", "signs", "ones", "zeros")
+
+
+def activity_tensor(pattern, shape, gen):
+    x = torch.randn(*shape, generator=gen, device="cuda", dtype=torch.float16)
+    if pattern == "randn":
+        return x
+    if pattern == "signs":
+        return torch.where(x > 0, 1.0, -1.0).to(torch.float16)
+    return torch.ones_like(x) if pattern == "ones" else torch.zeros_like(x)
+
+
+def activity_builders(quick, status, max_kv_gb=None):
+    """The prefill kernel and hipBLASLt's fp16 GEMM on the same shapes with
+    inputs of decreasing bit activity.  The instruction stream and control flow
+    hardly depend on the values (every tile is computed, and for all four
+    patterns the running maximum moves almost only on the first tile), so a
+    rate that rises as the inputs switch fewer bits shows a power-limited
+    clock, not an instruction-bound schedule."""
+    shapes = ([(1, 8, 2048, 128, True), (2, 8, 1024, 64, False)] if quick else
+              [(2, 32, 8192, 128, True), (2, 32, 8192, 128, False), (4, 16, 2048, 64, False)])
+    gemm_n = 2048 if quick else 8192
+    for pattern in ACTIVITY:
+        for (b, h, n, d, causal) in shapes:
+            def build(pattern=pattern, b=b, h=h, n=n, d=d, causal=causal):
+                g = torch.Generator(device="cuda").manual_seed(7)
+                q, k, v = (activity_tensor(pattern, (b, h, n, d), g) for _ in range(3))
+
+                def error(out):
+                    ref = akref.attention_fp32(q[:1, :1], k[:1, :1], v[:1, :1], causal)
+                    return (out[:1, :1].float() - ref).abs().max().item()
+                name = f"prefill {'causal ' if causal else ''}B={b} H={h} N={n} D={d}"
+                return Case("input_activity", dict(workload=name, data=pattern, batch=b, heads=h, seq=n, head_dim=d,
+                                                   causal=causal),
+                            4.0 * b * h * n * n * d * (0.5 if causal else 1.0), "TFLOP/s",
+                            {"flash_attention": lambda: ak.flash_attention(q, k, v, causal=causal)}, error)
+            yield build
+
+        def build_gemm(pattern=pattern, n=gemm_n):
+            g = torch.Generator(device="cuda").manual_seed(8)
+            a, b = (activity_tensor(pattern, (n, n), g) for _ in range(2))
+
+            def error(out):
+                ref = a[:64].float() @ b[:, :64].float()
+                return (out[:64, :64].float() - ref).abs().max().item()
+            return Case("input_activity", dict(workload=f"fp16 GEMM {n}^3", data=pattern), 2.0 * n ** 3, "TFLOP/s",
+                        {"hipblaslt_gemm": lambda: torch.mm(a, b)}, error)
+        yield build_gemm
+
+
 SECTIONS = {"prefill": prefill_builders, "decode": decode_builders, "decode_heads": decode_head_builders,
-            "split_ablation": ablation_builders, "ragged": ragged_builders}
+            "split_ablation": ablation_builders, "ragged": ragged_builders, "input_activity": activity_builders}
 
 
 # --------------------------------------------------------------- runner ----

@@ -368,9 +368,12 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
         if (t + 2 < nkt) load_kv<D, false, NW>(kb, kbuf + (t & 1) * T::TILE, (t + 2) * T::BN, n, ks, w, lane);
         // V(t+1) goes to the slot of V(t-1), last read before this barrier.  D = 64
         // issues it here; D = 128 after its QK^T phase, which spreads the CU's tile
-        // loads over the tile (+1-2% at D = 128, -8-10% at D = 64).
+        // loads over the tile (+1-2% at D = 128, -8-10% at D = 64).  Every body but
+        // the last has a next tile (t + 1 < nkt), so the guard is compile-time: a
+        // runtime branch after the QK^T phase let the compiler move the second
+        // unrolled body's exponentials out of the QK^T interleave, below the branch.
         constexpr bool V_LATE = D == 128;
-        if (!V_LATE && t + 1 < nkt)
+        if (!V_LATE && !LAST)
             load_kv<D, true, NW>(vb, vbuf + ((t + 1) & 1) * T::TILE, (t + 1) * T::BN, n, ks, w, lane);
         // Causal: a tile whose first key is after this wave's last row is skipped.
         const bool act = !MASK || !CAUSAL || t * T::BN <= qw0 + T::QW - 1;
@@ -408,7 +411,7 @@ __device__ __forceinline__ void prefill_qtile(const f16* __restrict__ qb, const 
             __builtin_amdgcn_sched_group_barrier(0x100, kKPrefetch, 0);
         }
         __builtin_amdgcn_s_setprio(0);
-        if (V_LATE && t + 1 < nkt)
+        if (V_LATE && !LAST)
             load_kv<D, true, NW>(vb, vbuf + ((t + 1) & 1) * T::TILE, (t + 1) * T::BN, n, ks, w, lane);
         if (act) {
             if constexpr (MAX_FIRST) {

@@ -151,6 +151,35 @@ def ablation_table(rows, section="split_ablation"):
     return _table(["Hq/Hkv", "B", "ctx", "best P", "best GB/s", "P:GB/s"], body)
 
 
+def activity_table(rows):
+    """TFLOP/s of each workload (columns) per input pattern (rows), and each
+    prefill workload's rate as a share of the GEMM's under the same inputs."""
+    sel = [r for r in rows if r["section"] == "input_activity"]
+    if not sel:
+        return ""
+    works, pats, by = [], [], {}
+    for r in sel:
+        if r["workload"] not in works:
+            works.append(r["workload"])
+        if r["data"] not in pats:
+            pats.append(r["data"])
+        by[(r["data"], r["workload"])] = r["tflops"]
+    gemm = next((w for w in works if "GEMM" in w), None)
+    pre = [w for w in works if w != gemm]
+    body = []
+    for p in pats:
+        cells = [p]
+        for w in works:
+            t = by.get((p, w))
+            cells.append(f"{t:.0f} ({100 * t / PEAK_TFLOPS:.0f}%)" if t is not None else "-")
+        g = by.get((p, gemm)) if gemm else None
+        for w in pre:
+            t = by.get((p, w))
+            cells.append(f"{100 * t / g:.0f}%" if t is not None and g else "-")
+        body.append(cells)
+    return _table(["inputs"] + [f"{w} TFLOP/s" for w in works] + [f"{w} / GEMM" for w in pre], body)
+
+
 def render(data):
     meta, rows = data["meta"], data["results"]
     lines = [f"# Attention kernels on {meta.get('gpu')} ({meta.get('arch')}, {meta.get('cu_count')} CUs)", ""]
@@ -185,6 +214,9 @@ def render(data):
     t = ablation_table(rows, "split_ablation_ragged")
     if t:
         lines += ["", "## Split-K partition ablation, mixed context lengths (ctx = max)", "", t]
+    t = activity_table(rows)
+    if t:
+        lines += ["", "## Rate against input bit activity (same kernels, same shapes)", "", t]
     t = worst_error_table(rows)
     if t:
         lines += ["", "## Worst error against fp32", "", t]

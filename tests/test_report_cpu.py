@@ -57,3 +57,19 @@ def test_committed_results_render():
     assert ours and all(r["max_abs_err"] < 4e-3 for r in ours)
     dec = [r for r in data["results"] if r["impl"] == "paged_split"]
     assert dec and all(r["max_abs_err"] < 2e-3 for r in dec)
+
+
+def test_activity_table():
+    rows = []
+    for data, pre, gemm in (("randn", 1000.0, 1250.0), ("zeros", 1400.0, 1750.0)):
+        rows.append(dict(section="input_activity", impl="flash_attention", workload="prefill causal N=8192",
+                         data=data, tflops=pre, ms=1.0, max_abs_err=1e-3))
+        rows.append(dict(section="input_activity", impl="hipblaslt_gemm", workload="fp16 GEMM 8192^3",
+                         data=data, tflops=gemm, ms=1.0, max_abs_err=0.0))
+    md = report.activity_table(rows)
+    assert "| inputs | prefill causal N=8192 TFLOP/s | fp16 GEMM 8192^3 TFLOP/s | prefill causal N=8192 / GEMM |" in md
+    assert "| randn | 1000 (40%) | 1250 (50%) | 80% |" in md
+    assert "| zeros | 1400 (56%) | 1750 (70%) | 80% |" in md
+    meta = dict(gpu="MI355X", arch="gfx950", cu_count=256, torch="x", hip="y", date="d", timing="t",
+                roofs=dict(copy_gbs=4000.0, fp16_gemm_tflops=1250.0), sdpa_backends={})
+    assert "## Rate against input bit activity" in report.render(dict(meta=meta, results=rows))
