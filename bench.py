@@ -22,7 +22,10 @@ mean launch duration (HIP events on the launch stream, inside the timed
 region), against the 2.5 PFLOP/s dense fp16 MFMA peak.  Every workload is
 also timed a second way, ``flushed``: K more steps, each after 512 MiB of
 device memory is overwritten (outside the step's start/end events), median
-reported, as the reference times every rep after an L2 flush.  ``cpu_baseline`` times
+reported, as the reference times every rep after an L2 flush.
+``measured_ceilings`` times hipBLASLt's 8192^3 fp16 GEMM and a 2 GiB device
+copy in the same run, the same way; each roofline also carries its rate as a
+fraction of the matching one (``frac_of_measured_ceiling``).  ``cpu_baseline`` times
 the numpy oracle (oracle/attention.py) on a bounded sample of the same
 workload on this host's cores.
 """
@@ -122,6 +125,31 @@ def timing_fields(t, steps, work, unit):
                         "value": round(rate(t["flushed_median_ms"]), 2), "unit": unit,
                         "frac_of_peak": round(rate(t["flushed_median_ms"]) / peak, 4)},
             "calls_before_timed": t["calls_before_timed"]}
+
+
+def measured_ceilings(steps, warmup):
+    """What this GPU sustains in the same run, timed like the workloads: an
+    8192^3 fp16 GEMM (hipBLASLt through torch.mm) on normal random inputs, and
+    a 2 GiB device-to-device copy (read + write bytes).  The reference's bench
+    reports its kernels against the same two ceilings (bench/bench.py:119-131)."""
+    import torch
+
+    n = 8192
+    g = torch.Generator(device="cuda").manual_seed(0)
+    a, b = (torch.randn(n, n, generator=g, device="cuda", dtype=torch.float16) for _ in range(2))
+    c = torch.empty_like(a)
+    t = timed_steps(lambda: torch.mm(a, b, out=c), steps, warmup)
+    gemm = 2.0 * n ** 3 / (t["mean_ms"] * 1e-3) / 1e12
+    del a, b, c
+    nbytes = 2 << 30
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    t = timed_steps(lambda: dst.copy_(src), steps, warmup)
+    copy = 2.0 * nbytes / (t["mean_ms"] * 1e-3) / 1e9
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"fp16_gemm": {"value": round(gemm, 1), "unit": "TFLOP/s", "what": "torch.mm 8192^3 fp16, N(0,1) inputs"},
+            "device_copy": {"value": round(copy, 1), "unit": "GB/s", "what": "2 GiB device-to-device copy, read + write"}}
 
 
 def prefill_case(b, h, n, d, causal, steps, warmup, seed=0):
@@ -402,6 +430,17 @@ def main():
         results[name] = cases[name]()
         log(json.dumps(results[name]))
     headline = results.get("prefill_d128_n8192_causal")
+    # Measured after the workloads, on the same GPU, when the headline runs (not
+    # in profiling runs of other workloads, whose traces it would lengthen).
+    ceil = measured_ceilings(K, W) if headline is not None else None
+    if ceil:
+        log(json.dumps({"measured_ceilings": ceil}))
+
+    def of_ceiling(ach, hbm):
+        if not ceil:
+            return None
+        return round(ach / ceil["device_copy" if hbm else "fp16_gemm"]["value"], 4)
+
     workloads = []
     for k, v in results.items():
         if k == "prefill_d128_n8192_causal":
@@ -412,7 +451,8 @@ def main():
         peak = PEAK_HBM_GBS if hbm else PEAK_FP16_TFLOPS
         workloads.append(dict(name=k, **v, roofline={
             "bound": "hbm" if hbm else "mfma", "achieved": ach, "peak": peak, "unit": v["unit"],
-            "frac": round(ach / peak, 4), "traffic": t["traffic_bytes"] if t else None}))
+            "frac": round(ach / peak, 4), "traffic": t["traffic_bytes"] if t else None,
+            "frac_of_measured_ceiling": of_ceiling(ach, hbm)}))
     cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
     from attnkernels import build as akbuild
     digest = akbuild.sources_digest()  # names the kernel sources measured (profiles cite it)
@@ -441,7 +481,10 @@ def main():
                      "traffic_source": "profiles/traffic.json (rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-scaled)",
                      "kernel": (measured_traffic("prefill_d128_n8192_causal") or {}).get("kernel",
                                                                                        "flash_prefill_kernel"),
-                     "kernel_ms_mean": headline["kernel_ms_mean"]},
+                     "kernel_ms_mean": headline["kernel_ms_mean"],
+                     # against the GEMM timed in this run (measured_ceilings)
+                     "frac_of_measured_ceiling": of_ceiling(ach, False)},
+        "measured_ceilings": ceil,
         "cpu_baseline": cpu,
         "workloads": workloads,
     }
