@@ -97,7 +97,8 @@ SETTLE_S = 0.25
 
 def timed_steps(fn, steps, warmup):
     """The driver's protocol (attnkernels.timing.steady_steps): settle, W warmup
-    steps, K back-to-back steps with one event per step boundary, then K
+    steps, the K timed back-to-back steps between a start and an end event,
+    K more steps with an event at each boundary (per-step median), then K
     flushed steps (512 MiB overwritten before each, outside its events)."""
     from attnkernels import timing
 
@@ -105,9 +106,10 @@ def timed_steps(fn, steps, warmup):
 
 
 def timing_fields(t, steps, work, unit):
-    """The per-workload timing columns: `value` from the K back-to-back steps
-    (wall clock), `kernel_*` from their step-boundary events, `flushed` from the
-    K flushed steps; `work` is FLOP (unit TFLOP/s) or bytes (GB/s) per step."""
+    """The per-workload timing columns: `value` from the K timed back-to-back
+    steps (wall clock), `kernel_ms_mean` from the two events around them,
+    `kernel_ms_median` from the marked steps, `flushed` from the K flushed
+    steps; `work` is FLOP (unit TFLOP/s) or bytes (GB/s) per step."""
     from attnkernels.timing import FLUSH_BYTES
 
     scale, peak = (1e12, PEAK_FP16_TFLOPS) if unit == "TFLOP/s" else (1e9, PEAK_HBM_GBS)

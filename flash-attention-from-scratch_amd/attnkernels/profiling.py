@@ -18,10 +18,11 @@ Only the dispatches of bench.py's K timed steps are summarised: bench.py
 reports ``calls_before_timed`` (accuracy call, settle and warmup calls), and
 every call launches each of this library's kernels once, so the timed
 dispatches of kernel X are its dispatches number calls_before_timed ..
-calls_before_timed + K - 1; the K flushed steps follow.  The trace-side step
+calls_before_timed + K - 1; K steps with an event at each boundary follow
+(bench.py's per-step median), then the K flushed steps.  The trace-side step
 time (start of one timed step's first kernel to the next one's) is the quantity
-bench.py's step-boundary events measure, so the two agree up to the profiler's
-own cost.
+bench.py's events around the timed steps measure, so the two agree up to the
+profiler's own cost.
 """
 from __future__ import annotations
 
@@ -131,7 +132,7 @@ def trace_summary(workload: str, raw: Path, out_dir: Path = PROFILES):
         raise SystemExit("no attnkernels dispatches in the trace")
     kstats, fstats = {}, {}
     for name, seq in per.items():
-        tw, fw = window(seq, n0, K), window(seq, n0 + K, K)
+        tw, fw = window(seq, n0, K), window(seq, n0 + 2 * K, K)
         if len(tw) != K:
             raise SystemExit(f"{name}: {len(seq)} dispatches, cannot take {K} timed ones from #{n0}")
         kstats[name] = stats_us([e - s for s, e, _ in tw])
@@ -180,7 +181,7 @@ def trace_summary(workload: str, raw: Path, out_dir: Path = PROFILES):
                      f"{st['max']:.1f} | {fm} |")
     lines += ["", f"Steps in the trace (start of one timed step's first kernel to the next one's, {K - 1} steps): "
                   f"mean {step_mean:.1f} us, median {step_med:.1f} us.",
-              f"bench.py in the same run (one HIP event per step boundary): mean "
+              f"bench.py in the same run (timed steps between two HIP events; median from marked steps): mean "
               f"{rec['kernel_ms_mean'] * 1e3:.1f} us, median {rec['kernel_ms_median'] * 1e3:.1f} us per step; "
               f"`ms_per_step` (wall clock) {rec['ms_per_step'] * 1e3:.1f} us."]
     if work:

@@ -42,9 +42,16 @@ def test_short_names():
 def test_trace_summary_takes_only_the_timed_steps(tmp_path):
     n0, K = 7, 5
     calls, t = [], 0
-    for i in range(n0 + 2 * K):
-        slow = i < n0  # settle / warmup calls are slower: they must not enter the stats
-        d = 300_000 if slow else 100_000 + 1000 * (i - n0)
+    # settle/warmup calls, the K timed steps, K marked steps, K flushed steps
+    for i in range(n0 + 3 * K):
+        if i < n0:
+            d = 300_000  # settle / warmup calls are slower: they must not enter the stats
+        elif i < n0 + K:
+            d = 100_000 + 1000 * (i - n0)
+        elif i < n0 + 2 * K:
+            d = 150_000  # marked steps: neither timed nor flushed
+        else:
+            d = 200_000  # flushed steps
         calls.append([(DEC, t, t + d), (RED, t + d + 2000, t + d + 7000)])
         t += d + 10_000
     raw = tmp_path / "raw"
@@ -65,6 +72,8 @@ def test_trace_summary_takes_only_the_timed_steps(tmp_path):
     assert step == pytest.approx(101.5 + 10.0)         # K-1 start-to-start periods: 100..103 us + 10 us gap
     text = out.read_text()
     assert "dispatches #7..#11" in text and "flushed median" in text
+    # the flushed column takes the last K calls, after the marked ones
+    assert "| paged_decode_kernel<128,4> | 5 | 102.0 | 102.0 | 100.0 | 104.0 | 200.0 |" in text
 
 
 def test_trace_summary_refuses_a_short_trace(tmp_path):
