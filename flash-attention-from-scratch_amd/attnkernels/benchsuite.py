@@ -380,11 +380,15 @@ def run_case(case: Case):
 
 
 def device_meta():
+    from attnkernels import build as akbuild
+
     p = torch.cuda.get_device_properties(0)
     return dict(gpu=p.name, arch=getattr(p, "gcnArchName", ""), cu_count=p.multi_processor_count,
                 memory_gb=round(p.total_memory / 2 ** 30, 1), torch=torch.__version__,
                 hip=getattr(torch.version, "hip", None), python=platform.python_version(),
-                host_cpus=os.cpu_count(), date=dt.datetime.now(dt.timezone.utc).strftime("%Y-%m-%d %H:%M UTC"))
+                host_cpus=os.cpu_count(), date=dt.datetime.now(dt.timezone.utc).strftime("%Y-%m-%d %H:%M UTC"),
+                # the kernel sources measured (the same digest bench.py and profiles/ cite)
+                sources_sha256=akbuild.sources_digest())
 
 
 def main(argv=None):

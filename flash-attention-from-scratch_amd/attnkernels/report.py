@@ -185,6 +185,8 @@ def render(data):
     lines = [f"# Attention kernels on {meta.get('gpu')} ({meta.get('arch')}, {meta.get('cu_count')} CUs)", ""]
     lines.append(f"torch {meta.get('torch')}, HIP {meta.get('hip')}, {meta.get('date')}.  "
                  f"Timing: {meta.get('timing')}.")
+    if meta.get("sources_sha256"):
+        lines.append(f"Kernel sources digest {meta['sources_sha256'][:12]}.")
     roofs = meta.get("roofs", {})
     lines += ["", f"Ceilings measured here: device copy {roofs.get('copy_gbs')} GB/s "
                   f"({100 * roofs.get('copy_gbs', 0) / PEAK_GBS:.0f}% of 8 TB/s), fp16 GEMM 8192^3 "
