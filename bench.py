@@ -154,14 +154,21 @@ def measured_ceilings(steps, warmup):
             "device_copy": {"value": round(copy, 1), "unit": "GB/s", "what": "2 GiB device-to-device copy, read + write"}}
 
 
+# Values of the dense prefill inputs (--inputs): the benchmark's are normal
+# random; the others switch fewer bits in the matrix core and exist for the
+# power-limit diagnostic (the same sweep as benchsuite's input_activity).
+INPUTS = "randn"
+
+
 def prefill_case(b, h, n, d, causal, steps, warmup, seed=0):
     import numpy as np
     import torch
 
     import attnkernels as ak
+    from attnkernels.benchsuite import activity_tensor
 
     g = torch.Generator(device="cuda").manual_seed(seed)
-    q, k, v = (torch.randn(b, h, n, d, generator=g, device="cuda", dtype=torch.float16) for _ in range(3))
+    q, k, v = (activity_tensor(INPUTS, (b, h, n, d), g) for _ in range(3))
     fn = lambda: ak.flash_attention(q, k, v, causal=causal)  # noqa: E731
     out = fn()
     torch.cuda.synchronize()
@@ -170,7 +177,8 @@ def prefill_case(b, h, n, d, causal, steps, warmup, seed=0):
     del out, ref
     t = timed_steps(fn, steps, warmup)
     flops = prefill_flops(b, h, n, d, causal)
-    res = dict(workload=f"prefill B={b} H={h} N={n} D={d} {'causal' if causal else 'non-causal'}",
+    res = dict(workload=f"prefill B={b} H={h} N={n} D={d} {'causal' if causal else 'non-causal'}"
+                        + ("" if INPUTS == "randn" else f" [{INPUTS} inputs]"),
                **timing_fields(t, steps, flops, "TFLOP/s"), flop_per_launch=flops, max_abs_err=float(f"{err:.3g}"))
     del q, k, v
     torch.cuda.empty_cache()
@@ -365,7 +373,7 @@ def cpu_configs():
 
 
 def main():
-    global SETTLE_S
+    global SETTLE_S, INPUTS
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
@@ -375,6 +383,9 @@ def main():
                     help="untimed calls of each workload before its warmup steps (clock settle)")
     ap.add_argument("--only", default="all",
                     help="all | headline | prefill | decode | comma list of workload names")
+    ap.add_argument("--inputs", choices=("randn", "signs", "ones", "zeros"), default="randn",
+                    help="values of the dense prefill inputs; the benchmark's are randn, the others are "
+                         "a diagnostic of the power-limited clock (fewer bits switching in the matrix core)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first run one plain 1 GiB device-to-device copy: the known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings to bytes")
@@ -401,6 +412,7 @@ def main():
         torch.cuda.empty_cache()
     K, W = args.steps, args.warmup
     SETTLE_S = max(0.0, args.settle_seconds)
+    INPUTS = args.inputs
     lens4 = torch.randint(1, 4097, (64,), generator=torch.Generator().manual_seed(4)).tolist()
     lensv = torch.randint(512, 8193, (16,), generator=torch.Generator().manual_seed(5)).tolist()
     cases = {  # BASELINE.json configs[1..4]
@@ -467,7 +479,8 @@ def main():
         "metric": "prefill TFLOP/s (% MFMA peak); paged decode KV GB/s (% HBM peak)",
         "value": headline["value"], "unit": "TFLOP/s", "n_gpus": 1, "steps": K, "warmup": W, "settle_s": SETTLE_S,
         "ms_per_step": headline["ms_per_step"], "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+        "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic" if INPUTS == "randn" else f"synthetic, prefill inputs all {INPUTS} (diagnostic, not the benchmark)",
         "config": {"workload": headline["workload"] + " (BASELINE configs[2])", "global_batch": 2,
                    "seq_len": 8192, "heads": 32, "head_dim": 128, "causal": True, "parallelism": "none"},
         "max_abs_err": headline["max_abs_err"],

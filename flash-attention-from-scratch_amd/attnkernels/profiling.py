@@ -76,6 +76,19 @@ def load_dispatches(path: Path):
     return [(short_name(r["Kernel_Name"]), int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r) for r in rows]
 
 
+# bench.py's diagnostic input patterns (--inputs): a workload named W_<pattern>
+# is bench.py's workload W run on those prefill inputs.
+INPUT_PATTERNS = ("signs", "ones", "zeros")
+
+
+def bench_args(workload: str) -> str:
+    """The bench.py arguments that select ``workload``."""
+    for p in INPUT_PATTERNS:
+        if workload.endswith("_" + p):
+            return f"--only {workload[:-len(p) - 1]} --inputs {p}"
+    return f"--only {workload}"
+
+
 def bench_record(path: Path, workload: str) -> dict:
     """The workload's entry in a bench.py JSON line (the headline line itself, or
     one of its ``workloads``)."""
@@ -161,17 +174,19 @@ def trace_summary(workload: str, raw: Path, out_dir: Path = PROFILES):
         for k, v in vals.items():
             traffic.setdefault(k, {})[which] = v
     cmd_dir = f"gpurun_out/praw/{workload}"
+    sel = bench_args(workload)
     lines = [f"# rocprofv3: {dom} on `{workload}`", "",
              f"Workload: {rec.get('workload')} (MI355X, one GPU; inputs resident in HBM).", "",
              f"Measured: {commit_note(rec.get('sources_sha256'))}.", "",
              "Commands (repository root on the GPU box, `export TMPDIR=/tmp`), then the summary on the host:", "",
              f"    rocprofv3 --kernel-trace --stats --output-format csv -d {cmd_dir} -o trace -- python bench.py "
-             f"--only {workload} --steps {K} --warmup {rec.get('warmup', 5)} --cpu-seconds 0 > {cmd_dir}/bench_trace.json",
-             f"    rocprofv3 --pmc FETCH_SIZE --output-format csv -d {cmd_dir} -o fetch -- python bench.py --only {workload} "
-             f"--steps 3 --warmup 1 --settle-seconds 0 --cpu-seconds 0 --calib-copy > {cmd_dir}/bench_fetch.json",
-             f"    rocprofv3 --pmc WRITE_SIZE --output-format csv -d {cmd_dir} -o write -- python bench.py --only {workload} "
-             f"--steps 3 --warmup 1 --settle-seconds 0 --cpu-seconds 0 --calib-copy > {cmd_dir}/bench_write.json",
-             f"    python flash-attention-from-scratch_amd/attnkernels/profiling.py trace {workload} {cmd_dir}", "",
+             f"{sel} --steps {K} --warmup {rec.get('warmup', 5)} --cpu-seconds 0 > {cmd_dir}/bench_trace.json"]
+    for which, counter in (("fetch", "FETCH_SIZE"), ("write", "WRITE_SIZE")):
+        if (raw / f"{which}_counter_collection.csv").exists():
+            lines.append(f"    rocprofv3 --pmc {counter} --output-format csv -d {cmd_dir} -o {which} -- python bench.py "
+                         f"{sel} --steps 3 --warmup 1 --settle-seconds 0 --cpu-seconds 0 --calib-copy "
+                         f"> {cmd_dir}/bench_{which}.json")
+    lines += [f"    python flash-attention-from-scratch_amd/attnkernels/profiling.py trace {workload} {cmd_dir}", "",
              f"## Kernel time over the {K} timed steps (`--kernel-trace`; dispatches #{n0}..#{n0 + K - 1} of each kernel)",
              "", "| kernel | dispatches | mean us | median us | min us | max us | flushed median us |",
              "|---|---:|---:|---:|---:|---:|---:|"]
@@ -272,7 +287,7 @@ def counters_summary(workload: str, raw: Path, passes, out_dir: Path = PROFILES)
             for n, v in c.items():
                 vals[k][(p, n)] = statistics.fmean(v[n0:n0 + K] or v)
         cmds.append(f"    rocprofv3 --pmc {' '.join(names)} --output-format csv -d gpurun_out/praw/{workload} -o {p} -- "
-                    f"python bench.py --only {workload} --steps {K} --warmup 1 --settle-seconds 0 --cpu-seconds 0 "
+                    f"python bench.py {bench_args(workload)} --steps {K} --warmup 1 --settle-seconds 0 --cpu-seconds 0 "
                     f"> gpurun_out/praw/{workload}/bench_{p}.json")
     outs = []
     for k, c in vals.items():

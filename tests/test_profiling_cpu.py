@@ -94,3 +94,9 @@ x.hip:80:1: remark:     Occupancy [waves/SIMD]: 8 [-Rpass-analysis=kernel-resour
 x.hip:80:1: remark:     LDS Size [bytes/block]: 2112 [-Rpass-analysis=kernel-resource-usage]"""
     u = build.parse_resource_usage(text)
     assert u == {"_ZN2ak19paged_decode_kernelILi64ELi1EEEv": {"VGPRs": 60, "Occupancy": 8, "LDS Size": 2112}}
+
+
+def test_bench_args_of_input_patterns():
+    assert profiling.bench_args("decode_gqa16_d128") == "--only decode_gqa16_d128"
+    assert profiling.bench_args("prefill_d128_n8192_causal_zeros") == "--only prefill_d128_n8192_causal --inputs zeros"
+    assert profiling.bench_args("prefill_d64_n2048_signs") == "--only prefill_d64_n2048 --inputs signs"
