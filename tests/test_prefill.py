@@ -113,13 +113,17 @@ def test_matches_cpu_sdpa(variant):
     assert max_err(out, sdpa) < TOL[64]
 
 
-@pytest.mark.parametrize("scale", [0.3, -0.05, 0.0, 1e-3])
+@pytest.mark.parametrize("scale", [0.3, -0.05, 0.0, 1e-3, 4.0, -30.0])
 @pytest.mark.parametrize("causal", [False, True])
-def test_explicit_scales(scale, causal):
-    q, k, v = rand_qkv(1, 2, 150, 128, seed=8)
+@pytest.mark.parametrize("d", [64, 128])
+def test_explicit_scales(scale, causal, d):
+    """Explicit scales, including large ones (scores in the hundreds of powers of
+    two: a nearly one-hot softmax whose running maximum keeps moving) and
+    negative ones (folded into Q's sign bits)."""
+    q, k, v = rand_qkv(1, 2, 150, d, seed=8)
     out = run("wmma64", q, k, v, causal, scale)
     ref = oracle.attention_fp32(q.numpy(), k.numpy(), v.numpy(), causal, scale)
-    assert max_err(out, ref) < TOL[128]
+    assert max_err(out, ref) < TOL[d]
 
 
 def test_rejects_bad_input():
