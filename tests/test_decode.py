@@ -102,13 +102,16 @@ def test_torch_baseline_matches():
     assert max_err(out, oracle.paged_decode_fp32(q, kc, vc, bt, cl)) < TOL[128]
 
 
-def test_scale_argument():
-    kc, vc, bt, cl = cache([700, 40], 2, 64)
-    q = rand_q(2, 4, 64)
+@pytest.mark.parametrize("d,hq,hkv", [(64, 4, 2), (128, 4, 4), (128, 16, 4), (64, 16, 2)])
+def test_scale_argument(d, hq, hkv):
+    """Explicit scales on both kernels, including large ones (a nearly one-hot
+    softmax: the per-wave reference maximum keeps moving) and negative ones."""
+    kc, vc, bt, cl = cache([700, 40], hkv, d)
+    q = rand_q(2, hq, d)
     qd, kcd, vcd, btd, cld = to_dev(q, kc, vc, bt, cl)
-    for s in (0.5, -0.1, 0.0):
+    for s in (0.5, -0.1, 0.0, 4.0, -30.0):
         out = ak.paged_decode(qd, kcd, vcd, btd, cld, 700, scale=s, partition_size=256)
-        assert max_err(out, oracle.paged_decode_fp32(q, kc, vc, bt, cl, scale=s)) < TOL[64]
+        assert max_err(out, oracle.paged_decode_fp32(q, kc, vc, bt, cl, scale=s)) < TOL[d], s
 
 
 def test_errors_match_reference():
