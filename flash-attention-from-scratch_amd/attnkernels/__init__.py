@@ -105,43 +105,60 @@ def _sm_count(device_index):
 # Split-count target of decode_partition.  The reference's rule aims at 4
 # blocks per SM (attnkernels/__init__.py:94-98, tuned on a T4).  The partition
 # is chosen from max_context_len alone (reading the lengths would cost a host
-# sync), so the rule must hold for uniform and for mixed-length batches.  The
-# MI355X split-K ablation of ``attnkernels.benchsuite`` (every power-of-two
-# partition; 12 uniform and 5 mixed-length batches over one, four and eight
-# query heads per kv head; results/mi355x.md) sets the three constants:
-#   * 8 workgroups per CU: uniform batches run fastest with few, long splits
-#     (256-512 workgroups in all), mixed batches with more (their short
-#     sequences leave most nominal splits empty);
-#   * at least 4 chunks (1024 tokens) per split where the context has them: a
-#     short split pays a workgroup's fixed costs (page ids, q, then K/V before
-#     any work; the merge; a partial for the reduce) for little work;
-#   * no split once B * Hkv reaches 2 workgroups per CU: the batch alone fills
-#     the GPU, and the reduce would only add a launch.
-# Together they reach 98% of the best partition on average, >= 87% in every
-# case (the old 16 per CU with 2-chunk splits: 95% and 82%).
-DECODE_WG_PER_CU = 8
-DECODE_MIN_CHUNKS = 4
+# sync), so the rule must hold for uniform, mixed-length and skewed batches.
+# The MI355X split-K ablation of ``attnkernels.benchsuite`` (every power-of-two
+# partition; 12 uniform, 5 mixed-length and 2 skewed batches (one long sequence
+# among short ones) over one, four and eight query heads per kv head;
+# results/mi355x.md), with the splits merged in the decode kernel, sets the
+# constants:
+#   * about one workgroup per CU in all: uniform batches run fastest with
+#     256-512 workgroups (B=1: 16-32 splits, B=4: 8, B=16: 2); every split pays
+#     a workgroup's fixed costs (page ids, q, then K/V before any work; the
+#     merge) for its share of the bytes;
+#   * splits of at most 4 chunks (1024 tokens): a long sequence among short
+#     ones (which the rule cannot see) is then cut into enough splits that it
+#     does not finish long after the rest;
+#   * no split once B * Hkv reaches 2 workgroups per CU and the context is at
+#     most 32 chunks (8192 tokens): the batch alone fills the GPU;
+#   * tokens per split a power-of-two number of chunks.
+# Together they reach 97% of the best partition on average and >= 85% in every
+# case (the previous rule, 8 per CU with 1024-token splits and no split at 2
+# per CU: 88% and 21%, on the skewed batch).
+DECODE_WG_PER_CU = 1
+DECODE_MIN_CHUNKS = 1
+DECODE_MAX_SPLIT_CHUNKS = 4
 DECODE_NO_SPLIT_BLOCKS_PER_CU = 2
+DECODE_NO_SPLIT_MAX_CHUNKS = 32
 REFERENCE_WG_PER_SM = 4
 
 
 def decode_partition(batch, num_kv_heads, max_context_len, device=None, wg_per_cu=DECODE_WG_PER_CU,
-                     min_chunks=DECODE_MIN_CHUNKS, no_split_blocks_per_cu=DECODE_NO_SPLIT_BLOCKS_PER_CU):
+                     min_chunks=DECODE_MIN_CHUNKS, no_split_blocks_per_cu=DECODE_NO_SPLIT_BLOCKS_PER_CU,
+                     no_split_max_chunks=DECODE_NO_SPLIT_MAX_CHUNKS, max_split_chunks=DECODE_MAX_SPLIT_CHUNKS,
+                     pow2_chunks=True):
     """Tokens per split for paged_decode: enough splits for about ``wg_per_cu``
-    workgroups per CU in total, at least ``min_chunks`` 256-token chunks per
-    split where the context has them, and one split once ``batch *
-    num_kv_heads`` reaches ``no_split_blocks_per_cu`` per CU (reference
-    attnkernels/__init__.py:93-101, whose rule is ``wg_per_cu=REFERENCE_WG_PER_SM,
-    min_chunks=1, no_split_blocks_per_cu=None``)."""
+    workgroups per CU in total, at least ``min_chunks`` and at most
+    ``max_split_chunks`` 256-token chunks per split (a power of two of them if
+    ``pow2_chunks``), and one split once ``batch * num_kv_heads`` reaches
+    ``no_split_blocks_per_cu`` per CU with at most ``no_split_max_chunks``
+    chunks of context (reference attnkernels/__init__.py:93-101, whose rule is
+    ``wg_per_cu=REFERENCE_WG_PER_SM, min_chunks=1, no_split_blocks_per_cu=None,
+    max_split_chunks=None, pow2_chunks=False``)."""
     dev = torch.cuda.current_device() if device is None else device
     blocks = batch * num_kv_heads
     cus = _sm_count(dev)
     max_chunks = -(-max_context_len // CHUNK)
-    if no_split_blocks_per_cu is not None and blocks >= no_split_blocks_per_cu * cus:
+    if (no_split_blocks_per_cu is not None and blocks >= no_split_blocks_per_cu * cus
+            and (no_split_max_chunks is None or max_chunks <= no_split_max_chunks)):
         return max(1, max_chunks) * CHUNK
     want = -(-int(wg_per_cu) * cus // blocks)
     splits = max(1, min(want, -(-max_chunks // int(min_chunks))))
-    return -(-max_chunks // splits) * CHUNK
+    chunks = -(-max_chunks // splits)
+    if max_split_chunks is not None:
+        chunks = min(chunks, int(max_split_chunks))
+    if pow2_chunks:
+        chunks = 1 << (chunks - 1).bit_length()
+    return chunks * CHUNK
 
 
 def paged_decode(q, k_cache, v_cache, block_tables, context_lens, max_context_len,

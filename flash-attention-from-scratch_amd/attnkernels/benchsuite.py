@@ -254,14 +254,17 @@ ABLATION_HEADS = ((32, 8), (32, 32), (64, 8))
 
 
 def ablation_builders(quick, status, max_kv_gb):
-    uniform = {(32, 8): ((1, 32768), (4, 8192), (16, 4096), (16, 8192), (64, 1024), (64, 4096)),
+    uniform = {(32, 8): ((1, 4096), (1, 16384), (1, 32768), (2, 4096), (4, 8192), (16, 4096), (16, 8192), (64, 1024),
+                         (64, 4096)),
                (32, 32): ((8, 32768), (16, 8192), (64, 4096)),
                (64, 8): ((1, 32768), (8, 8192), (64, 4096))}
     mixed = {(32, 8): ((4, 512, 32768, 1), (16, 512, 32768, 2), (64, 1, 4096, 3)),
              (32, 32): ((64, 1, 4096, 4),),
              (64, 8): ((16, 512, 32768, 5),)}
+    # one long sequence among many short ones, with B * Hkv >= 2 per CU
+    skewed = {(32, 8): ((64, 32768, 2048, 6),), (32, 32): ((32, 32768, 2048, 7),)}
     if quick:
-        uniform, mixed = {(32, 8): ((1, 8192),)}, {(32, 8): ((8, 512, 8192, 3),)}
+        uniform, mixed, skewed = {(32, 8): ((1, 8192),)}, {(32, 8): ((8, 512, 8192, 3),)}, {}
     for (hq, hkv), shapes in uniform.items():
         for B, c in shapes:
             if kv_gb([c] * B, hkv) > max_kv_gb:
@@ -275,6 +278,13 @@ def ablation_builders(quick, status, max_kv_gb):
             if kv_gb(lens, hkv) > max_kv_gb:
                 continue
             for p in partitions_up_to(max(lens)):
+                yield lambda lens=lens, p=p, hq=hq, hkv=hkv: decode_case(
+                    "split_ablation_ragged", lens, ("paged_split",), status, partition=p, hq=hq, hkv=hkv,
+                    extra=dict(ctx_lens=lens))
+    for (hq, hkv), shapes in skewed.items():
+        for B, long, short_hi, seed in shapes:
+            lens = [long] + mixed_lengths(B - 1, 1, short_hi, seed)
+            for p in partitions_up_to(long):
                 yield lambda lens=lens, p=p, hq=hq, hkv=hkv: decode_case(
                     "split_ablation_ragged", lens, ("paged_split",), status, partition=p, hq=hq, hkv=hkv,
                     extra=dict(ctx_lens=lens))

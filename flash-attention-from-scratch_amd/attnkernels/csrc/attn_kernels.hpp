@@ -36,6 +36,11 @@ struct DecodeArgs {
     float* o_part;         // [B, hq, S, D]  (S > 1 only)
     float* m_part;         // [B, hq, S]
     float* l_part;         // [B, hq, S]
+    // One int per (sequence, kv head), zero on entry and left zero: when set
+    // (and 1 < S <= kFusedMaxSplits), the last split of each (sequence, kv
+    // head) to finish merges the partials in the decode kernel, with no reduce
+    // launch.  Null: the reduce kernel merges them.
+    int32_t* counters;
     int64_t batch, hq, hkv, d, num_blocks, bs, max_blocks;
     int64_t partition, num_splits;
     float sl2;             // scale * log2(e)
@@ -60,7 +65,14 @@ hipError_t decode_launch(const DecodeArgs& a);
 // ak_paged_decode_noalloc, and its device address on the current GPU
 // (looked up once per device).
 constexpr size_t kDecodeScratchBytes = size_t(32) << 20;
-hipError_t decode_scratch(void** ptr);
+// Most splits merged in the decode kernel itself; more go to the reduce
+// kernel, whose workgroups per row read them in parallel (measured at B = 1-4,
+// Hq = 32, Hkv = 8: 8-16 splits merged in the kernel save 1.5 us a call, 32
+// break even, 64 lose 3 us).
+constexpr int64_t kFusedMaxSplits = 32;
+// Split counters of the static per-GPU array (sequences x query heads).
+constexpr size_t kDecodeScratchCounters = size_t(1) << 18;
+hipError_t decode_scratch(void** ptr, int32_t** counters);
 hipError_t cache_write_launch(const CacheWriteArgs& a);
 
 }  // namespace ak

@@ -128,7 +128,11 @@ int decode_args(const void* q, const void* k_cache, const void* v_cache, const i
     return ok();
 }
 
-// Split partials laid out in one fp32 buffer: o [B, Hq, S, D], m [B, Hq, S], l [B, Hq, S].
+// Bytes of the split partials in one fp32 buffer: o [B, Hq, S, D], m [B, Hq, S], l [B, Hq, S].
+size_t partials_bytes(int64_t batch, int64_t num_heads, int64_t splits, int64_t head_dim) {
+    return (size_t)batch * (size_t)num_heads * (size_t)splits * (size_t)(head_dim + 2) * sizeof(float);
+}
+
 void set_partials(ak::DecodeArgs& a, void* buf) {
     float* ws = static_cast<float*>(buf);
     const size_t rows = (size_t)a.batch * (size_t)a.hq * (size_t)a.num_splits;
@@ -143,7 +147,7 @@ extern "C" {
 
 const char* ak_last_error(void) { return g_last_error.c_str(); }
 
-int ak_abi_version(void) { return 100; }
+int ak_abi_version(void) { return 101; }
 
 int ak_naive_attention(const void* q, const void* k, const void* v, void* o, int64_t batch,
                        int64_t heads, int64_t seq_len, int64_t head_dim, int causal, double scale,
@@ -196,7 +200,7 @@ size_t ak_paged_decode_workspace_size(int64_t batch, int64_t num_heads, int64_t 
     if (batch < 0 || num_heads < 0 || head_dim <= 0 || max_context_len < 1 || partition <= 0) return 0;
     const int64_t splits = (max_context_len + partition - 1) / partition;
     if (splits <= 1) return 0;
-    return (size_t)batch * (size_t)num_heads * (size_t)splits * (size_t)(head_dim + 2) * sizeof(float);
+    return partials_bytes(batch, num_heads, splits, head_dim);
 }
 
 int ak_paged_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_tables,
@@ -204,11 +208,26 @@ int ak_paged_decode(const void* q, const void* k_cache, const void* v_cache, con
                     int64_t num_kv_heads, int64_t head_dim, int64_t num_blocks, int64_t block_size,
                     int64_t max_blocks_per_seq, int64_t max_context_len, double scale, int64_t partition,
                     void* workspace, size_t workspace_bytes, void* stream) {
+    return ak_paged_decode_fused(q, k_cache, v_cache, block_tables, context_lens, out, batch, num_heads,
+                                 num_kv_heads, head_dim, num_blocks, block_size, max_blocks_per_seq,
+                                 max_context_len, scale, partition, workspace, workspace_bytes, nullptr, 0, stream);
+}
+
+int ak_paged_decode_fused(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_tables,
+                          const int32_t* context_lens, void* out, int64_t batch, int64_t num_heads,
+                          int64_t num_kv_heads, int64_t head_dim, int64_t num_blocks, int64_t block_size,
+                          int64_t max_blocks_per_seq, int64_t max_context_len, double scale, int64_t partition,
+                          void* workspace, size_t workspace_bytes, int32_t* counters, int64_t counters_len,
+                          void* stream) {
     ak::DecodeArgs a{};
     const int rc = decode_args(q, k_cache, v_cache, block_tables, context_lens, out, batch, num_heads, num_kv_heads,
                                head_dim, num_blocks, block_size, max_blocks_per_seq, max_context_len, scale,
                                partition, stream, a);
     if (rc != AK_OK || batch == 0) return rc;
+    if (counters && (counters_len < batch * num_kv_heads || (reinterpret_cast<uintptr_t>(counters) & 3u)))
+        return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: counters must be a 4-byte aligned int32 array of at least "
+                                             "batch * num_kv_heads = " + std::to_string(batch * num_kv_heads) +
+                                             " elements");
     if (a.num_splits > 1) {
         const size_t need = ak_paged_decode_workspace_size(batch, num_heads, head_dim, max_context_len, partition);
         if (!workspace || workspace_bytes < need)
@@ -217,6 +236,7 @@ int ak_paged_decode(const void* q, const void* k_cache, const void* v_cache, con
         if (!aligned16(workspace))
             return fail(AK_ERR_INVALID_ARGUMENT, "paged_decode: workspace must be 16-byte aligned");
         set_partials(a, workspace);
+        a.counters = counters;
     }
     return hip_status(ak::decode_launch(a), "paged_decode");
 }
@@ -232,7 +252,7 @@ int ak_paged_decode_noalloc(const void* q, const void* k_cache, const void* v_ca
                                partition, stream, a);
     if (rc != AK_OK || batch == 0) return rc;
     if (a.num_splits > 1) {
-        const size_t need = ak_paged_decode_workspace_size(batch, num_heads, head_dim, max_context_len, partition);
+        const size_t need = partials_bytes(batch, num_heads, a.num_splits, head_dim);
         if (need > ak::kDecodeScratchBytes)
             return fail(AK_ERR_WORKSPACE, "paged_decode_noalloc: the split partials need " + std::to_string(need) +
                                               " bytes, more than the static scratch of " +
@@ -250,9 +270,13 @@ int ak_paged_decode_noalloc(const void* q, const void* k_cache, const void* v_ca
                             "paged_decode_noalloc: the stream must belong to the current device");
         }
         void* ws = nullptr;
-        const hipError_t e = ak::decode_scratch(&ws);
+        int32_t* counters = nullptr;
+        const hipError_t e = ak::decode_scratch(&ws, &counters);
         if (e != hipSuccess) return hip_status(e, "paged_decode_noalloc");
         set_partials(a, ws);
+        // counters for every (sequence, kv head) fit the static array: merged in
+        // the decode kernel; otherwise by the reduce kernel
+        if ((size_t)batch * (size_t)num_kv_heads <= ak::kDecodeScratchCounters) a.counters = counters;
     }
     return hip_status(ak::decode_launch(a), "paged_decode_noalloc");
 }

@@ -27,10 +27,185 @@
 #include "attn_kernels.hpp"
 #include "wave.hpp"
 
-#include <mutex>
 #include <type_traits>
 
 namespace ak {
+
+// Agent-coherent (sc1) loads and stores of split partials: relaxed atomics at
+// agent scope reach the device-wide coherence point without the whole-cache
+// writeback and invalidate that release/acquire fences cost on gfx950.
+__device__ __forceinline__ void coherent_store(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float coherent_load(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ f32x4 coherent_load4(const float* p) {  // 16-byte aligned
+    const uint64_t a = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t b = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p) + 1, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    const f32x2 x = __builtin_bit_cast(f32x2, a), y = __builtin_bit_cast(f32x2, b);
+    return f32x4{x[0], x[1], y[0], y[1]};
+}
+
+// Merge of the ns split partials of one (sequence, kv head) into its G output
+// rows row0 .. row0 + G - 1, by one workgroup: the LSE rule of the reduce
+// kernel below (paged_decode.cu:204-215), M = max m_s, w_s = l_s 2^(m_s - M),
+// O = sum w_s o_s / sum w_s, with partials of l = 0 weighted 0.  A thread owns
+// 4 head dims of one row (a unit) and every SG-th split; its loads for NB of
+// them at a time are issued together and merged by a running maximum, and the
+// SG split groups of a unit are merged through LDS.
+template <int D, int G, int THREADS>
+__device__ __forceinline__ void merge_splits(const float* o_part, const float* m_part, const float* l_part,
+                                             f16* out, size_t row0, int num_splits, int ns, int tid) {
+    // NB: loads per batch, enough for the most splits merged here in one batch,
+    // but no more than the kernel's main loop has registers for (8, or 16 for
+    // the four- and eight-head kernels)
+    constexpr int UNITS = G * D / 4, SG = THREADS / UNITS;
+    constexpr int NB_CAP = G >= 4 ? 16 : 8, NB_ALL = (int)((kFusedMaxSplits + SG - 1) / SG);
+    constexpr int NB = NB_ALL < NB_CAP ? NB_ALL : NB_CAP;
+    static_assert(SG >= 1 && SG * UNITS == THREADS, "units tile the workgroup");
+    __shared__ float mg_m[THREADS], mg_l[THREADS];
+    __shared__ f32x4 mg_o[THREADS];
+    const int u = tid % UNITS, sg = tid / UNITS;
+    const int h = u / (D / 4), d4 = u % (D / 4);
+    const size_t row = row0 + h;
+    const float* mp = m_part + row * num_splits;
+    const float* lp = l_part + row * num_splits;
+    const float* op = o_part + row * num_splits * D + d4 * 4;
+    float M = -INFINITY, L = 0.f;
+    f32x4 O = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = sg; s0 < ns; s0 += SG * NB) {
+        float ms[NB], ls[NB];
+        f32x4 os[NB];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int s = s0 + j * SG;
+            const bool in = s < ns;
+            ms[j] = in ? coherent_load(mp + s) : -INFINITY;
+            ls[j] = in ? coherent_load(lp + s) : 0.f;
+            os[j] = in ? coherent_load4(op + (size_t)s * D) : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        float mb = M;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) mb = fmaxf(mb, ls[j] > 0.f ? ms[j] : -INFINITY);
+        if (mb == -INFINITY) continue;  // no weighted partial yet
+        const float a = exp2_fast(M - mb);  // 0 while M = -inf
+        L *= a;
+        O *= a;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const float wgt = ls[j] > 0.f ? ls[j] * exp2_fast(ms[j] - mb) : 0.f;
+            L += wgt;
+            O += wgt * os[j];
+        }
+        M = mb;
+    }
+    if constexpr (SG > 1) {
+        mg_m[tid] = M;
+        mg_l[tid] = L;
+        mg_o[tid] = O;
+        __syncthreads();
+        if (sg == 0) {
+            float Mx = M;
+#pragma unroll
+            for (int k = 1; k < SG; ++k) Mx = fmaxf(Mx, mg_m[k * UNITS + u]);
+            const float Mu = Mx == -INFINITY ? 0.f : Mx;
+            L = 0.f;
+            O = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k = 0; k < SG; ++k) {
+                const float wgt = exp2_fast(mg_m[k * UNITS + u] - Mu);  // groups without weight: 2^-inf = 0
+                L += mg_l[k * UNITS + u] * wgt;
+                O += wgt * mg_o[k * UNITS + u];
+            }
+        }
+    }
+    if (sg == 0) {
+        const float inv = L > 0.f ? 1.f / L : 0.f;  // a row with no weight at all is written as zeros
+        f16* dst = out + row * D + d4 * 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[i] = (f16)(O[i] * inv);
+    }
+}
+
+// Split epilogue of both decode kernels.  red_acc / red_m / red_l hold the
+// workgroup's per-wave (acc, m, l) of the kv head's G query heads (m in the
+// log2 domain; the stored l is L * lscale).  The waves are merged by the LSE
+// rule, then:
+//   * one split in the launch (num_splits == 1), or (fused) one split with
+//     tokens for this sequence: the fp16 output rows;
+//   * reduce path (counters == null): the split's partial (normalised o, m, l)
+//     for the reduce kernel;
+//   * fused path: the partial with agent-coherent stores, then, once they are
+//     complete, the (sequence, kv head) counter.  The split that takes it to
+//     ns - 1 is the last to arrive: every other partial is complete, so it
+//     merges all ns of them into the output and resets the counter to zero
+//     for the next call.  No workgroup waits for another.
+template <int D, int G, int NW>
+__device__ __forceinline__ void split_epilogue(const float (&red_acc)[NW][G][D], const float (&red_m)[NW][G],
+                                               const float (&red_l)[NW][G], float lscale, f16* __restrict__ out,
+                                               float* __restrict__ o_part, float* __restrict__ m_part,
+                                               float* __restrict__ l_part, int32_t* __restrict__ counters, int b,
+                                               int kvh, int hkv, int split, int num_splits, int ns, int tid) {
+    constexpr int THREADS = NW * kWave;
+    __shared__ int last;
+    const int hq = hkv * G;
+    const bool direct = num_splits == 1 || (counters && ns == 1);
+    const bool fused = counters && !direct;
+    for (int idx = tid; idx < G * D; idx += THREADS) {
+        const int h = idx / D, d = idx % D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < NW; ++v) M = fmaxf(M, red_m[v][h]);
+        // A split whose every token sits on an out-of-range page has no valid
+        // token in any wave: M stays -inf, and subtracting it would give
+        // 2^(-inf + inf) = NaN.  Such a split yields o = 0, l = 0, m = -inf,
+        // which the merge weighs 0.
+        const float Mu = M == -INFINITY ? 0.f : M;
+        float L = 0.f, o = 0.f;
+#pragma unroll
+        for (int v = 0; v < NW; ++v) {
+            const float wv = exp2_fast(red_m[v][h] - Mu);  // waves without tokens: 2^-inf = 0
+            L += red_l[v][h] * wv;
+            o += red_acc[v][h][d] * wv;
+        }
+        o = L > 0.f ? o / L : 0.f;
+        const size_t row = (size_t)b * hq + kvh * G + h;
+        const size_t slot = row * num_splits + split;
+        if (direct) {
+            out[row * D + d] = (f16)o;
+        } else if (!fused) {
+            o_part[slot * D + d] = o;
+            if (d == 0) {
+                m_part[slot] = M;
+                l_part[slot] = L * lscale;
+            }
+        } else {
+            coherent_store(o_part + slot * D + d, o);
+            if (d == 0) {
+                coherent_store(m_part + slot, M);
+                coherent_store(l_part + slot, L * lscale);
+            }
+        }
+    }
+    if (!fused) return;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores are complete
+    __syncthreads();
+    int32_t* cnt = counters + (size_t)b * hkv + kvh;
+    if (tid == 0) last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ns - 1;
+    __syncthreads();
+    if (!last) return;
+    merge_splits<D, G, THREADS>(o_part, m_part, l_part, out, (size_t)b * hq + (size_t)kvh * G, num_splits, ns, tid);
+    if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Splits of sequence b that hold tokens (the reduce kernel reads as many).
+__device__ __forceinline__ int splits_with_tokens(int ctx, int partition, int num_splits) {
+    const int ns = ctx > 0 ? (int)(((long long)ctx + partition - 1) / partition) : 0;
+    return min(ns, num_splits);
+}
 
 // One query head per kv head (the reference's decode configurations).
 template <int D>
@@ -59,8 +234,8 @@ __global__ void __launch_bounds__((DecodeTile<D>::THREADS))
 paged_decode_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const f16* __restrict__ vc,
                     const int* __restrict__ block_tables, const int* __restrict__ ctx_lens,
                     f16* __restrict__ out, float* __restrict__ o_part, float* __restrict__ m_part,
-                    float* __restrict__ l_part, int hkv, int bs, int bs_shift, int max_blocks,
-                    int num_blocks, int partition, int num_splits, float sl2) {
+                    float* __restrict__ l_part, int32_t* __restrict__ counters, int hkv, int bs, int bs_shift,
+                    int max_blocks, int num_blocks, int partition, int num_splits, float sl2) {
     using T = DecodeTile<D>;
     constexpr int G = 1;
     __shared__ float red_acc[T::NW][G][D];
@@ -101,7 +276,7 @@ paged_decode_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const
     if (start >= ctx) {  // whole workgroup: this split is past the context
         // A sequence with no context (outside the >= 1 contract) gets a zero row,
         // as the reduce gives it when there are several splits.
-        if (num_splits == 1)
+        if (num_splits == 1 || (counters && split == 0))
             for (int idx = tid; idx < D; idx += T::THREADS) out[((size_t)b * hq + kvh) * D + idx] = (f16)0.f;
         return;
     }
@@ -185,35 +360,8 @@ paged_decode_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const
         }
     }
     __syncthreads();
-    for (int idx = tid; idx < G * D; idx += T::THREADS) {
-        const int h = idx / D, d = idx % D;
-        float M = -INFINITY;
-#pragma unroll
-        for (int v = 0; v < T::NW; ++v) M = fmaxf(M, red_m[v][h]);
-        // A split whose every token sits on an out-of-range page has no valid
-        // token in any wave: M stays -inf, and subtracting it would give
-        // 2^(-inf + inf) = NaN.  Such a split yields o = 0, l = 0, m = -inf,
-        // which the reduce weighs 0.
-        const float Mu = M == -INFINITY ? 0.f : M;
-        float L = 0.f, o = 0.f;
-#pragma unroll
-        for (int v = 0; v < T::NW; ++v) {
-            const float wv = exp2_fast(red_m[v][h] - Mu);  // waves without tokens: 2^-inf = 0
-            L += red_l[v][h] * wv;
-            o += red_acc[v][h][d] * wv;
-        }
-        o = L > 0.f ? o / L : 0.f;
-        const size_t row = (size_t)b * hq + kvh * G + h;
-        if (num_splits == 1) {
-            out[row * D + d] = (f16)o;
-        } else {
-            o_part[(row * num_splits + split) * D + d] = o;
-            if (d == 0) {
-                m_part[row * num_splits + split] = M;
-                l_part[row * num_splits + split] = L;
-            }
-        }
-    }
+    split_epilogue<D, G, T::NW>(red_acc, red_m, red_l, 1.f, out, o_part, m_part, l_part, counters, b, kvh, hkv,
+                                split, num_splits, splits_with_tokens(ctx, partition, num_splits), tid);
 }
 
 // ---------------------------------------------------------------------------
@@ -340,8 +488,8 @@ __global__ void __launch_bounds__((GqaTile<D, G>::THREADS))
 paged_decode_gqa_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const f16* __restrict__ vc,
                         const int* __restrict__ block_tables, const int* __restrict__ ctx_lens,
                         f16* __restrict__ out, float* __restrict__ o_part, float* __restrict__ m_part,
-                        float* __restrict__ l_part, int hkv, int bs, int bs_shift, int max_blocks,
-                        int num_blocks, int partition, int num_splits, float sl2) {
+                        float* __restrict__ l_part, int32_t* __restrict__ counters, int hkv, int bs,
+                        int bs_shift, int max_blocks, int num_blocks, int partition, int num_splits, float sl2) {
     using T = GqaTile<D, G>;
     constexpr int U = T::U, N = T::N, S = T::S, LB = T::LB;
     // P = 2^(s - m + kPShift): the largest P the fast path accepts is 2^kPMax.
@@ -396,7 +544,7 @@ paged_decode_gqa_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, c
 
     const int ctx = min(ctx_raw, max_tok);
     if (start >= ctx) {
-        if (num_splits == 1)
+        if (num_splits == 1 || (counters && split == 0))
             for (int idx = tid; idx < G * D; idx += T::THREADS)
                 out[((size_t)b * hq + kvh * G + idx / D) * D + idx % D] = (f16)0.f;
         return;
@@ -586,33 +734,10 @@ paged_decode_gqa_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, c
         red_l[w][fh] = l_own;
     }
     __syncthreads();
-    for (int idx = tid; idx < G * D; idx += T::THREADS) {
-        const int h = idx / D, d = idx % D;
-        float M = -INFINITY;
-#pragma unroll
-        for (int v = 0; v < T::NW; ++v) M = fmaxf(M, red_m[v][h]);
-        const float Mu = M == -INFINITY ? 0.f : M;
-        float L = 0.f, o = 0.f;
-#pragma unroll
-        for (int v = 0; v < T::NW; ++v) {
-            const float wv = exp2_fast(red_m[v][h] - Mu);
-            L += red_l[v][h] * wv;
-            o += red_acc[v][h][d] * wv;
-        }
-        o = L > 0.f ? o / L : 0.f;
-        const size_t row = (size_t)b * hq + kvh * G + h;
-        if (num_splits == 1) {
-            out[row * D + d] = (f16)o;
-        } else {
-            o_part[(row * num_splits + split) * D + d] = o;
-            if (d == 0) {
-                // m in the log2 domain of the scores, as the reduce expects:
-                // the kPShift on P cancels in o and is taken out of l here.
-                m_part[row * num_splits + split] = M;
-                l_part[row * num_splits + split] = L * (1.f / 128.f);
-            }
-        }
-    }
+    // m in the log2 domain of the scores: the kPShift on P cancels in o and is
+    // taken out of l here.
+    split_epilogue<D, G, T::NW>(red_acc, red_m, red_l, 1.f / 128.f, out, o_part, m_part, l_part, counters, b, kvh,
+                                hkv, split, num_splits, splits_with_tokens(ctx, partition, num_splits), tid);
 }
 
 // LSE merge of the split partials (paged_decode.cu:204-215): one 256-thread
@@ -688,19 +813,22 @@ static hipError_t launch_decode(const DecodeArgs& a) {
         if ((int64_t(1) << s) == a.bs) bs_shift = s;
     const hipStream_t stream = (hipStream_t)a.stream;
     dim3 grid((unsigned)a.hkv, (unsigned)a.num_splits, (unsigned)a.batch);
+    // Few enough splits: the last split of each (sequence, kv head) merges them
+    // in the decode kernel (no reduce launch); otherwise the reduce kernel does.
+    int32_t* counters = a.counters && a.num_splits > 1 && a.num_splits <= kFusedMaxSplits ? a.counters : nullptr;
     if constexpr (G == 1)
         hipLaunchKernelGGL((paged_decode_kernel<D>), grid, dim3(DecodeTile<D>::THREADS), 0, stream, (const f16*)a.q,
                            (const f16*)a.k_cache, (const f16*)a.v_cache, a.block_tables, a.context_lens,
-                           (f16*)a.out, a.o_part, a.m_part, a.l_part, (int)a.hkv, (int)a.bs, bs_shift,
+                           (f16*)a.out, a.o_part, a.m_part, a.l_part, counters, (int)a.hkv, (int)a.bs, bs_shift,
                            (int)a.max_blocks, (int)a.num_blocks, (int)a.partition, (int)a.num_splits, a.sl2);
     else
         hipLaunchKernelGGL((paged_decode_gqa_kernel<D, G>), grid, dim3(GqaTile<D, G>::THREADS), 0, stream,
                            (const f16*)a.q, (const f16*)a.k_cache, (const f16*)a.v_cache, a.block_tables,
-                           a.context_lens, (f16*)a.out, a.o_part, a.m_part, a.l_part, (int)a.hkv, (int)a.bs,
-                           bs_shift, (int)a.max_blocks, (int)a.num_blocks, (int)a.partition,
+                           a.context_lens, (f16*)a.out, a.o_part, a.m_part, a.l_part, counters, (int)a.hkv,
+                           (int)a.bs, bs_shift, (int)a.max_blocks, (int)a.num_blocks, (int)a.partition,
                            (int)a.num_splits, a.sl2);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || a.num_splits == 1) return e;
+    if (e != hipSuccess || a.num_splits == 1 || counters) return e;
     hipLaunchKernelGGL((paged_reduce_kernel<D>), dim3((unsigned)(a.batch * a.hq)), dim3(256), 0, stream,
                        a.o_part, a.m_part, a.l_part, a.context_lens, (f16*)a.out, (int)a.hq,
                        (int)a.partition, (int)a.num_splits, (int)(a.max_blocks * a.bs));
@@ -710,31 +838,28 @@ static hipError_t launch_decode(const DecodeArgs& a) {
 // Split partials of ak_paged_decode_noalloc: one static array per GPU, held
 // until the process ends, so that callers that cannot allocate (graph capture,
 // tight serving loops) need no workspace.  Every call on a GPU shares that
-// GPU's array; calls that overlap on one GPU race.  Nothing in it has to start
-// at zero: the reduce reads only partials the same call's decode kernel wrote.
+// GPU's array; calls that overlap on one GPU race.  The partials need no
+// initial contents: a merge reads only partials the same call wrote.  The
+// split counters (one per sequence and kv head) start at zero, as every
+// static device array does, and every call leaves them at zero.
 static __device__ __align__(256) float scratch[kDecodeScratchBytes / sizeof(float)];
+static __device__ __align__(256) int32_t scratch_counters[kDecodeScratchCounters];
 
-// Device address of this GPU's scratch array.  In host code `scratch` names a
-// host-side stand-in, never the device memory: the address comes from
-// hipGetSymbolAddress, called once per device with that device current, and
-// only that pointer is handed to kernels.
-hipError_t decode_scratch(void** ptr) {
-    constexpr int kMaxDevices = 64;
-    static std::mutex mu;
-    static void* addr[kMaxDevices] = {};
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
+// Device addresses of this GPU's scratch arrays.  In host code `scratch` and
+// `scratch_counters` name host-side stand-ins, never the device memory: the
+// addresses come from hipGetSymbolAddress with the device current, and only
+// those pointers are handed to kernels.  They are looked up again on every
+// call (a lookup allocates nothing), so they stay valid across a
+// hipDeviceReset that reloads the module.
+hipError_t decode_scratch(void** ptr, int32_t** counters) {
+    void* p = nullptr;
+    void* c = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e == hipSuccess) e = hipGetSymbolAddress(&c, HIP_SYMBOL(scratch_counters));
     if (e != hipSuccess) return e;
-    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
-    std::lock_guard<std::mutex> lock(mu);
-    if (!addr[dev]) {
-        void* p = nullptr;
-        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (e != hipSuccess) return e;
-        if (!p) return hipErrorInvalidSymbol;
-        addr[dev] = p;
-    }
-    *ptr = addr[dev];
+    if (!p || !c) return hipErrorInvalidSymbol;
+    *ptr = p;
+    *counters = static_cast<int32_t*>(c);
     return hipSuccess;
 }
 

@@ -10,6 +10,11 @@
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 
+#include <map>
+#include <mutex>
+#include <utility>
+#include <vector>
+
 #include "attnkernels.h"
 
 namespace {
@@ -28,6 +33,23 @@ void check_prefill(const torch::Tensor& q, const torch::Tensor& k, const torch::
 
 void* stream_of(const torch::Tensor& t) {
     return at::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.device().index()).stream();
+}
+
+// Split counters of the decode kernels' in-kernel merge, one array per
+// (device, stream): zeroed when allocated, and every decode call leaves its
+// counters at zero, so the calls on a stream (which run in order) share it.
+// A stream that needs more counters gets a new, larger array; the smaller one
+// is kept, because a captured graph may still use it.
+torch::Tensor split_counters(const torch::Tensor& q, int64_t n) {
+    static std::mutex mu;
+    static std::map<std::pair<int, void*>, std::vector<torch::Tensor>> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    auto& arrays = cache[{(int)q.device().index(), stream_of(q)}];
+    if (arrays.empty() || arrays.back().numel() < n) {
+        const int64_t grow = arrays.empty() ? 0 : 2 * arrays.back().numel();
+        arrays.push_back(torch::zeros({std::max(n, std::max<int64_t>(grow, 4096))}, q.options().dtype(torch::kInt)));
+    }
+    return arrays.back();
 }
 
 }  // namespace
@@ -113,14 +135,18 @@ torch::Tensor paged_decode(torch::Tensor q, torch::Tensor kc, torch::Tensor vc, 
         TORCH_CHECK(t->device() == q.device(), "all paged_decode tensors must be on the same device");
     const at::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     auto out = torch::empty_like(q);
-    const int64_t B = q.size(0), hq = q.size(1), D = q.size(2);
+    const int64_t B = q.size(0), hq = q.size(1), D = q.size(2), hkv = kc.size(1);
     const size_t ws_bytes = ak_paged_decode_workspace_size(B, hq, D, max_ctx, partition);
-    torch::Tensor ws;
-    if (ws_bytes > 0) ws = torch::empty({(int64_t)ws_bytes}, q.options().dtype(torch::kByte));
-    check_rc(ak_paged_decode(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr<int32_t>(),
-                             ctx.data_ptr<int32_t>(), out.data_ptr(), B, hq, kc.size(1), D, kc.size(0), kc.size(2),
-                             bt.size(1), max_ctx, scale, partition, ws_bytes ? ws.data_ptr() : nullptr, ws_bytes,
-                             stream_of(q)));
+    torch::Tensor ws, counters;
+    if (ws_bytes > 0) {
+        ws = torch::empty({(int64_t)ws_bytes}, q.options().dtype(torch::kByte));
+        counters = split_counters(q, B * hkv);
+    }
+    check_rc(ak_paged_decode_fused(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr<int32_t>(),
+                                   ctx.data_ptr<int32_t>(), out.data_ptr(), B, hq, hkv, D, kc.size(0), kc.size(2),
+                                   bt.size(1), max_ctx, scale, partition, ws_bytes ? ws.data_ptr() : nullptr,
+                                   ws_bytes, ws_bytes ? counters.data_ptr<int32_t>() : nullptr,
+                                   ws_bytes ? counters.numel() : 0, stream_of(q)));
     return out;
 }
 

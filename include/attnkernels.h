@@ -116,6 +116,27 @@ int ak_paged_decode(const void *q, const void *k_cache, const void *v_cache,
                     int64_t max_context_len, double scale, int64_t partition, void *workspace,
                     size_t workspace_bytes, void *stream);
 
+/* ak_paged_decode with the split merge in the decode kernel itself: no
+ * separate reduce launch (about 4 us of a small decode step).  No counterpart
+ * in the reference, which always launches paged_reduce_kernel
+ * (attnkernels/csrc/paged_decode.cu:243-248).  The last split of each
+ * (sequence, kv head) to finish merges the partials, which needs one int32
+ * counter per (sequence, kv head):
+ *   counters:     device int32 array of counters_len >= batch * num_kv_heads
+ *                 elements, all zero before the first call; every call leaves
+ *                 them zero, so one array serves any later call on the same
+ *                 stream (calls that share it must not overlap).  NULL: the
+ *                 reduce kernel merges, exactly as ak_paged_decode.
+ * Launches with more than 64 splits merge in the reduce kernel either way
+ * (its workgroups per row read the partials in parallel).  Arguments, results
+ * and errors are otherwise those of ak_paged_decode. */
+int ak_paged_decode_fused(const void *q, const void *k_cache, const void *v_cache,
+                          const int32_t *block_tables, const int32_t *context_lens, void *out,
+                          int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                          int64_t num_blocks, int64_t block_size, int64_t max_blocks_per_seq,
+                          int64_t max_context_len, double scale, int64_t partition, void *workspace,
+                          size_t workspace_bytes, int32_t *counters, int64_t counters_len, void *stream);
+
 /* Paged-KV decode that allocates nothing: ak_paged_decode without the
  * workspace arguments.  No counterpart in the reference; it is for callers
  * that cannot allocate device memory (code under HIP graph capture, tight

@@ -46,46 +46,62 @@ def test_paged_decode_validation():
         ak.paged_decode(q, kc[..., :32].contiguous(), kc[..., :32].contiguous(), bt, lens, 1)
 
 
+# decode_partition keywords that give the reference's rule (attnkernels/__init__.py:93-101)
+REFERENCE_RULE = dict(wg_per_cu=ak.REFERENCE_WG_PER_SM, min_chunks=1, no_split_blocks_per_cu=None,
+                      max_split_chunks=None, pow2_chunks=False)
+# and the previous default of this build
+PREVIOUS_RULE = dict(wg_per_cu=8, min_chunks=4, no_split_blocks_per_cu=2, no_split_max_chunks=None,
+                     max_split_chunks=None, pow2_chunks=False)
+
+
 def test_decode_partition_matches_reference_t4_run(monkeypatch):
     fx = json.loads((GOLDEN / "decode_partition_t4.json").read_text())
     monkeypatch.setattr(ak, "_sm_count", lambda dev: fx["sm_count"])
     for r in fx["rows"]:
-        assert ak.decode_partition(r["batch"], r["num_kv_heads"], r["max_context_len"], 0,
-                                   wg_per_cu=ak.REFERENCE_WG_PER_SM, min_chunks=1,
-                                   no_split_blocks_per_cu=None) == r["partition"], r
+        assert ak.decode_partition(r["batch"], r["num_kv_heads"], r["max_context_len"], 0, **REFERENCE_RULE) \
+            == r["partition"], r
 
 
 def test_decode_partition_on_256_cus(monkeypatch):
     monkeypatch.setattr(ak, "_sm_count", lambda dev: 256)
     for b, hkv, ctx in [(64, 32, 4096), (8, 32, 32768), (1, 8, 32768), (3, 8, 1), (64, 8, 1024), (16, 8, 8192)]:
-        assert ak.decode_partition(b, hkv, ctx, 0, min_chunks=1, no_split_blocks_per_cu=None) == \
-            oracle.decode_partition(b, hkv, ctx, 256, wg_per_sm=ak.DECODE_WG_PER_CU)
-        assert ak.decode_partition(b, hkv, ctx, 0, wg_per_cu=4, min_chunks=1, no_split_blocks_per_cu=None) == \
-            oracle.decode_partition(b, hkv, ctx, 256)
-    assert (ak.DECODE_WG_PER_CU, ak.DECODE_MIN_CHUNKS, ak.DECODE_NO_SPLIT_BLOCKS_PER_CU) == (8, 4, 2)
-    # The floor of 4 chunks per split: 256 splits wanted but 32 at most (128
-    # chunks); 16 wanted, 8 at most (32 chunks); short contexts keep one split.
-    assert oracle.decode_partition(1, 8, 32768, 256, wg_per_sm=8) == 256
+        for wg in (1, 4, 8):
+            assert ak.decode_partition(b, hkv, ctx, 0, **dict(REFERENCE_RULE, wg_per_cu=wg)) == \
+                oracle.decode_partition(b, hkv, ctx, 256, wg_per_sm=wg)
+    assert (ak.DECODE_WG_PER_CU, ak.DECODE_MIN_CHUNKS, ak.DECODE_MAX_SPLIT_CHUNKS, ak.DECODE_NO_SPLIT_BLOCKS_PER_CU,
+            ak.DECODE_NO_SPLIT_MAX_CHUNKS) == (1, 1, 4, 2, 32)
+    # About one workgroup per CU: 32 splits for 8 (sequence, kv head) blocks,
+    # two for 128, one for 504; at most 4 chunks (1024 tokens) per split, a
+    # power of two of them.
+    assert ak.decode_partition(1, 8, 4096, 0) == 256
+    assert ak.decode_partition(1, 8, 16384, 0) == 512
     assert ak.decode_partition(1, 8, 32768, 0) == 1024
-    assert oracle.decode_partition(16, 8, 8192, 256, wg_per_sm=8) == 512
+    assert ak.decode_partition(1, 8, 65536, 0) == 1024    # 64 splits: capped at 4 chunks
     assert ak.decode_partition(16, 8, 8192, 0) == 1024
     assert ak.decode_partition(3, 8, 1, 0) == 256
-    assert ak.decode_partition(3, 8, 300, 0) == 512
-    # No split once batch * kv heads reaches 2 per CU (512 here).
-    assert oracle.decode_partition(64, 8, 1024, 256, wg_per_sm=8) == 256
+    assert ak.decode_partition(3, 8, 300, 0) == 256
+    assert ak.decode_partition(4, 8, 3000, 0) == 512      # 12 chunks over 8 splits: 2 chunks
+    assert ak.decode_partition(63, 8, 4096, 0) == 1024    # 504 blocks: still split
+    # No split once batch * kv heads reaches 2 per CU (512 here) with at most
+    # 8192 tokens of context ...
     assert ak.decode_partition(64, 8, 1024, 0) == 1024
     assert ak.decode_partition(64, 32, 4096, 0) == 4096
-    assert ak.decode_partition(63, 8, 4096, 0) == 1024   # 504 blocks: still split
+    assert ak.decode_partition(64, 8, 8192, 0) == 8192
+    # ... but a longer context may be one long sequence among short ones: split
+    # it (the previous rule ran such a batch unsplit, at 21% of the best rate)
+    assert ak.decode_partition(64, 8, 32768, 0) == 1024
+    assert ak.decode_partition(64, 8, 32768, 0, **PREVIOUS_RULE) == 32768
 
 
 def test_decode_partition_default_is_near_the_measured_optimum(monkeypatch):
     """On 256 CUs the default rule picks, over every case of the MI355X split-K
     ablation (tests/golden/decode_partition_mi355x.json: bandwidth of every
-    power-of-two partition, uniform and mixed context lengths, one, four and
-    eight query heads per kv head), a partition within 13% of the fastest one
-    in every case and within 3% on average; the reference's rule and the
-    previous default (16 per CU, 2-chunk floor, always split) do worse on
-    average."""
+    power-of-two partition, uniform, mixed and skewed context lengths, one,
+    four and eight query heads per kv head), a partition within 15% of the
+    fastest one in every case and within 3% on average; the reference's rule
+    does worse on average, and the previous default (8 per CU, 4-chunk floor,
+    no split at 2 per CU whatever the context) on average and in the worst
+    case."""
     fx = json.loads((GOLDEN / "decode_partition_mi355x.json").read_text())
     monkeypatch.setattr(ak, "_sm_count", lambda dev: fx["cu_count"])
     assert fx["rows"] and any(r["mixed_lengths"] for r in fx["rows"])
@@ -111,9 +127,10 @@ def test_decode_partition_default_is_near_the_measured_optimum(monkeypatch):
         return min(fr), sum(fr) / len(fr)
 
     worst, mean = fractions()
-    assert worst >= 0.87 and mean >= 0.97
-    assert fractions(wg_per_cu=ak.REFERENCE_WG_PER_SM, min_chunks=1, no_split_blocks_per_cu=None)[1] < mean
-    assert fractions(wg_per_cu=16, min_chunks=2, no_split_blocks_per_cu=None)[1] < mean
+    assert worst >= 0.85 and mean >= 0.97
+    assert fractions(**REFERENCE_RULE)[1] < mean
+    prev_worst, prev_mean = fractions(**PREVIOUS_RULE)
+    assert prev_mean < mean and prev_worst < worst
 
 
 def test_reference_module_attention_matches_oracle():

@@ -34,6 +34,7 @@ def lib():
     L.ak_paged_decode.argtypes = [vp] * 6 + [i64] * 8 + [f64, i64, vp, ctypes.c_size_t, vp]
     L.ak_reshape_and_cache.argtypes = [vp] * 5 + [i64] * 7 + [vp]
     L.ak_paged_decode_noalloc.argtypes = [vp] * 6 + [i64] * 8 + [f64, i64, vp]
+    L.ak_paged_decode_fused.argtypes = [vp] * 6 + [i64] * 8 + [f64, i64, vp, ctypes.c_size_t, vp, i64, vp]
     L.ak_prefill_gqa.argtypes = [vp] * 4 + [i64] * 5 + [ctypes.c_int, f64, vp]
     L.ak_prefill_varlen.argtypes = [vp] * 5 + [i64] * 6 + [ctypes.c_int, f64, vp]
     return L
@@ -49,7 +50,7 @@ def test_header_declares_the_reference_entry_points():
 def test_library_exports_every_declared_symbol(lib):
     for name in declared_functions():
         assert hasattr(lib, name), name
-    assert lib.ak_abi_version() == 100
+    assert lib.ak_abi_version() == 101
 
 
 FAKE = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
@@ -163,3 +164,14 @@ def test_noalloc_decode_rejects_oversized_partials_before_any_hip_call(lib):
     # the shared validation still applies first
     assert lib.ak_paged_decode_noalloc(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1, 6, 4, 128, 100, 16, 8, 100,
                                        0.1, 256, None) == 1
+
+
+def test_fused_decode_validates_counters_before_any_hip_call(lib):
+    """ak_paged_decode_fused rejects a counter array shorter than batch *
+    num_kv_heads, or misaligned, before touching the GPU."""
+    need = lib.ak_paged_decode_workspace_size(2, 8, 128, 1000, 256)
+    args = [FAKE] * 6 + [2, 8, 4, 128, 64, 16, 63, 1000, 0.1, 256, FAKE, need]
+    assert lib.ak_paged_decode_fused(*args, FAKE, 7, None) == 1
+    assert b"counters" in lib.ak_last_error()
+    assert lib.ak_paged_decode_fused(*args, ctypes.c_void_p(4098), 8, None) == 1
+    assert b"counters" in lib.ak_last_error()

@@ -1,8 +1,10 @@
-"""ak_paged_decode_noalloc (static per-GPU split partials, no workspace argument)
-against ak_paged_decode with a caller workspace, through the C-ABI: the same
-kernels, so the outputs must be bit-identical, and both must match the oracle.
+"""ak_paged_decode_noalloc (static per-GPU split partials and split counters,
+no workspace argument) against ak_paged_decode_fused with a caller workspace
+and counter array, through the C-ABI: the same kernels, so the outputs must be
+bit-identical; both must match the oracle and the two-kernel ak_paged_decode.
 Two calls in a row, the second with a smaller input, show that the shared
-static array carries nothing from one call into the next."""
+static arrays carry nothing from one call into the next.  A call allocates no
+device memory, and one captured in a HIP graph replays bit-identically."""
 import ctypes
 
 import numpy as np
@@ -26,6 +28,7 @@ def lib():
     L.ak_paged_decode_workspace_size.argtypes = [i64] * 5
     L.ak_paged_decode_workspace_size.restype = ctypes.c_size_t
     L.ak_paged_decode.argtypes = [vp] * 6 + [i64] * 8 + [f64, i64, vp, ctypes.c_size_t, vp]
+    L.ak_paged_decode_fused.argtypes = [vp] * 6 + [i64] * 8 + [f64, i64, vp, ctypes.c_size_t, vp, i64, vp]
     L.ak_paged_decode_noalloc.argtypes = [vp] * 6 + [i64] * 8 + [f64, i64, vp]
     return L
 
@@ -38,27 +41,44 @@ def stream():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
-def one_case(lib, lens, hq, hkv, d, partition, seed):
-    print(f"noalloc case lens={lens} hq={hq} hkv={hkv} d={d} P={partition}", flush=True)
+def make_case(lens, hq, hkv, d, seed):
     kc, vc, bt, cl = oracle.make_paged_cache(lens, hkv, d, block_size=16, extra_blocks=3, seed=seed)
     q = np.random.default_rng(seed + 1).standard_normal((len(lens), hq, d), dtype=np.float32).astype(np.float16)
-    qd, kcd, vcd, btd, cld = (torch.from_numpy(a).cuda() for a in (q, kc, vc, bt, cl))
+    dev = [torch.from_numpy(a).cuda() for a in (q, kc, vc, bt, cl)]
+    sizes = [len(lens), hq, hkv, d, kc.shape[0], 16, bt.shape[1], max(lens)]
+    return (q, kc, vc, bt, cl), dev, sizes
+
+
+def noalloc(lib, dev, sizes, out, partition):
+    qd, kcd, vcd, btd, cld = dev
+    return lib.ak_paged_decode_noalloc(ptr(qd), ptr(kcd), ptr(vcd), ptr(btd), ptr(cld), ptr(out), *sizes,
+                                       sizes[3] ** -0.5, partition, stream())
+
+
+def one_case(lib, lens, hq, hkv, d, partition, seed):
+    print(f"noalloc case lens={lens} hq={hq} hkv={hkv} d={d} P={partition}", flush=True)
+    (q, kc, vc, bt, cl), dev, sizes = make_case(lens, hq, hkv, d, seed)
+    qd, kcd, vcd, btd, cld = dev
     max_ctx = max(lens)
-    sizes = [len(lens), hq, hkv, d, kc.shape[0], 16, bt.shape[1], max_ctx]
     need = lib.ak_paged_decode_workspace_size(len(lens), hq, d, max_ctx, partition)
     assert 0 < need <= MAX_BYTES
     ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    counters = torch.zeros(len(lens) * hkv, dtype=torch.int32, device="cuda")
     want = torch.empty_like(qd)
-    rc = lib.ak_paged_decode(ptr(qd), ptr(kcd), ptr(vcd), ptr(btd), ptr(cld), ptr(want), *sizes, d ** -0.5,
+    rc = lib.ak_paged_decode_fused(ptr(qd), ptr(kcd), ptr(vcd), ptr(btd), ptr(cld), ptr(want), *sizes,
+                                   d ** -0.5, partition, ptr(ws), need, ptr(counters), counters.numel(), stream())
+    assert rc == 0, lib.ak_last_error()
+    plain = torch.empty_like(qd)
+    rc = lib.ak_paged_decode(ptr(qd), ptr(kcd), ptr(vcd), ptr(btd), ptr(cld), ptr(plain), *sizes, d ** -0.5,
                              partition, ptr(ws), need, stream())
     assert rc == 0, lib.ak_last_error()
     got = torch.full_like(qd, float("nan"))
-    rc = lib.ak_paged_decode_noalloc(ptr(qd), ptr(kcd), ptr(vcd), ptr(btd), ptr(cld), ptr(got), *sizes,
-                                     d ** -0.5, partition, stream())
-    assert rc == 0, lib.ak_last_error()
+    assert noalloc(lib, dev, sizes, got, partition) == 0, lib.ak_last_error()
     torch.cuda.synchronize()
     assert torch.equal(got, want)
-    assert max_err(got, oracle.paged_decode_fp32(q, kc, vc, bt, cl)) < TOL[d]
+    ref = oracle.paged_decode_fp32(q, kc, vc, bt, cl)
+    assert max_err(got, ref) < TOL[d]
+    assert max_err(plain, ref) < TOL[d]
 
 
 def test_noalloc_matches_workspace_entry_point_twice(lib):
@@ -76,3 +96,45 @@ def test_noalloc_rejects_partials_beyond_the_static_array(lib):
                                      0.1, 256, None)
     assert rc == 3
     assert b"static scratch" in lib.ak_last_error()
+
+
+def test_noalloc_allocates_no_device_memory(lib):
+    """Free device memory (hipMemGetInfo) is the same before and after a call;
+    a first call loads the module and its static arrays, so it runs first."""
+    _, dev, sizes = make_case([2000, 500], 16, 4, 128, seed=81)
+    out = torch.empty_like(dev[0])
+    assert noalloc(lib, dev, sizes, out, 256) == 0, lib.ak_last_error()
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    for _ in range(3):
+        assert noalloc(lib, dev, sizes, out, 256) == 0, lib.ak_last_error()
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info()
+    assert free1 == free0
+
+
+def test_noalloc_under_graph_capture_replays_bit_identically(lib):
+    """A noalloc call captured in a HIP graph (stream capture through torch):
+    each replay, with eager noalloc calls of another shape between them, gives
+    the eager result bit for bit."""
+    (q, kc, vc, bt, cl), dev, sizes = make_case([3000, 1200, 40], 32, 8, 128, seed=91)
+    eager = torch.empty_like(dev[0])
+    assert noalloc(lib, dev, sizes, eager, 256) == 0, lib.ak_last_error()
+    torch.cuda.synchronize()
+    assert max_err(eager, oracle.paged_decode_fp32(q, kc, vc, bt, cl)) < TOL[128]
+    out = torch.full_like(dev[0], float("nan"))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        rc = noalloc(lib, dev, sizes, out, 256)
+    assert rc == 0, lib.ak_last_error()
+    _, other_dev, other_sizes = make_case([700, 700], 16, 16, 64, seed=93)
+    other = torch.empty_like(other_dev[0])
+    for _ in range(3):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        assert noalloc(lib, other_dev, other_sizes, other, 256) == 0, lib.ak_last_error()
+        torch.cuda.synchronize()
