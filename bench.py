@@ -23,9 +23,11 @@ region), against the 2.5 PFLOP/s dense fp16 MFMA peak.  Every workload is
 also timed a second way, ``flushed``: K more steps, each after 512 MiB of
 device memory is overwritten (outside the step's start/end events), median
 reported, as the reference times every rep after an L2 flush.
-``measured_ceilings`` times hipBLASLt's 8192^3 fp16 GEMM and a 2 GiB device
-copy in the same run, the same way; each roofline also carries its rate as a
-fraction of the matching one (``frac_of_measured_ceiling``).  ``cpu_baseline`` times
+``measured_ceilings`` times hipBLASLt's 8192^3 fp16 GEMM, a 2 GiB device copy
+and a 2 GiB read-only stream in the same run, the same way; each roofline also
+carries its rate as a fraction of the matching one (``frac_of_measured_ceiling``:
+prefill against the GEMM, decode against the read stream, the cache writer
+against the copy).  ``cpu_baseline`` times
 the numpy oracle (oracle/attention.py) on a bounded sample of the same
 workload on this host's cores.
 """
@@ -131,10 +133,15 @@ def timing_fields(t, steps, work, unit):
 
 def measured_ceilings(steps, warmup):
     """What this GPU sustains in the same run, timed like the workloads: an
-    8192^3 fp16 GEMM (hipBLASLt through torch.mm) on normal random inputs, and
-    a 2 GiB device-to-device copy (read + write bytes).  The reference's bench
-    reports its kernels against the same two ceilings (bench/bench.py:119-131)."""
+    8192^3 fp16 GEMM (hipBLASLt through torch.mm) on normal random inputs, a
+    2 GiB device-to-device copy (read + write bytes), and 2 GiB read once by
+    the library's streaming checksum.  The reference's bench reports its
+    kernels against a GEMM and a copy (bench/bench.py:119-131); decode only
+    reads, and reads faster than a copy moves, so its rates are reported
+    against the read stream."""
     import torch
+
+    import attnkernels as ak
 
     n = 8192
     g = torch.Generator(device="cuda").manual_seed(0)
@@ -148,10 +155,18 @@ def measured_ceilings(steps, warmup):
     dst = torch.empty_like(src)
     t = timed_steps(lambda: dst.copy_(src), steps, warmup)
     copy = 2.0 * nbytes / (t["mean_ms"] * 1e-3) / 1e9
-    del src, dst
+    del dst
+    ext = ak.load_extension()
+    acc = torch.zeros(4, dtype=torch.int32, device="cuda")
+    t = timed_steps(lambda: ext.stream_checksum(src, acc), steps, warmup)
+    read = nbytes / (t["mean_ms"] * 1e-3) / 1e9
+    del src
     torch.cuda.empty_cache()
     return {"fp16_gemm": {"value": round(gemm, 1), "unit": "TFLOP/s", "what": "torch.mm 8192^3 fp16, N(0,1) inputs"},
-            "device_copy": {"value": round(copy, 1), "unit": "GB/s", "what": "2 GiB device-to-device copy, read + write"}}
+            "device_copy": {"value": round(copy, 1), "unit": "GB/s", "what": "2 GiB device-to-device copy, read + write"},
+            "read_stream": {"value": round(read, 1), "unit": "GB/s",
+                            "what": "2 GiB read once (ak_stream_checksum: a contiguous chunk per CU, 16-byte "
+                                    "non-temporal loads, 16 in flight per lane); the ceiling of the decode kernels, which only read their K/V"}}
 
 
 # Values of the dense prefill inputs (--inputs): the benchmark's are normal
@@ -309,6 +324,8 @@ def cpu_baseline(seconds):
 
     import oracle
 
+    import torch
+
     try:
         from threadpoolctl import threadpool_info
         threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
@@ -325,19 +342,24 @@ def cpu_baseline(seconds):
         if time.perf_counter() - t0 >= seconds:
             break
     el = time.perf_counter() - t0
+    log(f"cpu oracle: {done} slices of causal N={n} D={d} in {el:.1f} s")
     flops = oracle.prefill_flops(1, done, n, d, True)
     return dict(value=round(flops / el / 1e12, 5), unit="TFLOP/s", cores=int(threads), kind="port",
                 sample=f"{done} (batch, head) slices of causal N=8192 D=128 through the numpy fp32 "
                        f"oracle, {el:.1f} s, os.cpu_count()={os.cpu_count()}",
+                os_cpu_count=os.cpu_count(), torch_num_threads=torch.get_num_threads(), blas_threads=int(threads),
                 configs=cpu_configs())
 
 
 def cpu_configs():
     """The same oracle on the other reference configurations (wall time,
-    time.perf_counter, median of several runs; nothing extrapolated):
-    prefill B=1 H=4 N=256 D=64 and B=4 H=16 N=2048 D=64 (non-causal, scale
-    1/8) whole, and paged decode on the first 8 of the 64 ragged sequences
-    of the decode workload (same seeded lengths, Hq=Hkv=32, D=128, pages of 16)."""
+    time.perf_counter; nothing extrapolated): prefill B=1 H=4 N=256 D=64 and
+    B=4 H=16 N=2048 D=64 (non-causal, scale 1/8) whole; the ragged paged
+    decode of configs[3] whole (the bench's 64 seeded lengths, Hq=Hkv=32,
+    D=128, pages of 16); and one whole sequence of the long decode of
+    configs[4] at D=128 and D=64 (32768 tokens, 32 heads; the batch holds 8
+    such sequences).  A configuration runs once, and twice more (the median
+    is reported) when one run takes under 3 s."""
     import statistics
 
     import numpy as np
@@ -345,30 +367,51 @@ def cpu_configs():
 
     import oracle
 
-    def median_s(fn, runs):
+    def median_s(fn):
         ts = []
-        for _ in range(runs):
+        while len(ts) < (1 if ts and ts[0] >= 3.0 else 3):
             t0 = time.perf_counter()
             fn()
             ts.append(time.perf_counter() - t0)
-        return statistics.median(ts)
+        return statistics.median(ts), len(ts)
+
+    def paged_cache(lens, h, d, bs, seed):
+        # the caches are drawn on the GPU and copied to host memory: drawing
+        # 10^8-10^9 normals on the host takes longer than the oracle itself
+        nblk = [-(-n // bs) for n in lens]
+        total = sum(nblk) + len(lens)
+        perm = torch.randperm(total, generator=torch.Generator().manual_seed(seed)).to(torch.int32).numpy()
+        tables = np.zeros((len(lens), max(nblk)), np.int32)
+        pos = 0
+        for b, nb in enumerate(nblk):
+            tables[b, :nb] = perm[pos:pos + nb]
+            pos += nb
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        kc, vc = (torch.randn((total, h, bs, d), generator=g, device="cuda", dtype=torch.float16).cpu().numpy()
+                  for _ in range(2))
+        return kc, vc, tables, np.asarray(lens, np.int32)
 
     rng = np.random.default_rng(1)
     rows = []
-    for (b, h, n, d, runs) in ((1, 4, 256, 64, 5), (4, 16, 2048, 64, 3)):
+    for (b, h, n, d) in ((1, 4, 256, 64), (4, 16, 2048, 64)):
         q, k, v = (rng.standard_normal((b, h, n, d), dtype=np.float32).astype(np.float16) for _ in range(3))
-        sec = median_s(lambda: oracle.attention_fp32(q, k, v, False, 0.125), runs)
+        sec, runs = median_s(lambda: oracle.attention_fp32(q, k, v, False, 0.125))
+        log(f"cpu oracle: prefill B={b} H={h} N={n} D={d} {sec:.2f} s ({runs} runs)")
         rows.append(dict(config=f"prefill B={b} H={h} N={n} D={d} non-causal",
                          value=round(oracle.prefill_flops(b, h, n, d, False) / sec / 1e12, 5), unit="TFLOP/s",
-                         seconds=round(sec, 4), runs=runs, stat="median"))
-    lens = torch.randint(1, 4097, (64,), generator=torch.Generator().manual_seed(4)).tolist()[:8]
-    kc, vc, bt, cl = oracle.make_paged_cache(lens, 32, 128, 16, seed=4)
-    qd = rng.standard_normal((len(lens), 32, 128), dtype=np.float32).astype(np.float16)
-    sec = median_s(lambda: oracle.paged_decode_fp32(qd, kc, vc, bt, cl), 3)
-    rows.append(dict(config=f"paged decode, first 8 of the 64 ragged sequences (sum_ctx={sum(lens)}) "
-                            "Hq=Hkv=32 D=128 bs=16",
-                     value=round(oracle.decode_kv_bytes(lens, 32, 128) / sec / 1e9, 3), unit="GB/s",
-                     seconds=round(sec, 4), runs=3, stat="median"))
+                         seconds=round(sec, 4), runs=runs, stat="median" if runs > 1 else "single run"))
+    lens4 = torch.randint(1, 4097, (64,), generator=torch.Generator().manual_seed(4)).tolist()
+    for lens, d, what in ((lens4, 128, "configs[3] paged decode, all 64 ragged sequences"),
+                          ([32768], 128, "configs[4] paged decode D=128, one whole 32768-token sequence"),
+                          ([32768], 64, "configs[4] paged decode D=64, one whole 32768-token sequence")):
+        kc, vc, bt, cl = paged_cache(lens, 32, d, 16, seed=4)
+        qd = rng.standard_normal((len(lens), 32, d), dtype=np.float32).astype(np.float16)
+        sec, runs = median_s(lambda: oracle.paged_decode_fp32(qd, kc, vc, bt, cl))
+        log(f"cpu oracle: {what} {sec:.2f} s ({runs} runs)")
+        rows.append(dict(config=f"{what} (sum_ctx={sum(lens)}) Hq=Hkv=32 D={d} bs=16",
+                         value=round(oracle.decode_kv_bytes(lens, 32, d) / sec / 1e9, 3), unit="GB/s",
+                         seconds=round(sec, 4), runs=runs, stat="median" if runs > 1 else "single run"))
+        del kc, vc
     return rows
 
 
@@ -450,10 +493,10 @@ def main():
     if ceil:
         log(json.dumps({"measured_ceilings": ceil}))
 
-    def of_ceiling(ach, hbm):
+    def of_ceiling(ach, hbm, decode=False):
         if not ceil:
             return None
-        return round(ach / ceil["device_copy" if hbm else "fp16_gemm"]["value"], 4)
+        return round(ach / ceil[("read_stream" if decode else "device_copy") if hbm else "fp16_gemm"]["value"], 4)
 
     workloads = []
     for k, v in results.items():
@@ -466,7 +509,7 @@ def main():
         workloads.append(dict(name=k, **v, roofline={
             "bound": "hbm" if hbm else "mfma", "achieved": ach, "peak": peak, "unit": v["unit"],
             "frac": round(ach / peak, 4), "traffic": t["traffic_bytes"] if t else None,
-            "frac_of_measured_ceiling": of_ceiling(ach, hbm)}))
+            "frac_of_measured_ceiling": of_ceiling(ach, hbm, k.startswith("decode"))}))
     cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
     from attnkernels import build as akbuild
     digest = akbuild.sources_digest()  # names the kernel sources measured (profiles cite it)

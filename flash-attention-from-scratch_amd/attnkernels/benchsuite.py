@@ -205,6 +205,16 @@ def decode_case(section, lens, impl_names, status, partition=None, hq=LAYER["hq"
     def error(out):
         out = out.reshape(B, hq, d)
         return max((out[b:b + 1].float() - refs[b].reshape(1, hq, d)).abs().max().item() for b in check)
+    if "paged_split" in impl_names and hq > hkv:
+        # The grouped-query kernels round P to fp16; the one-head kernel keeps
+        # it in fp32.  The same queries through the one-head kernel, on caches
+        # whose kv heads are repeated once per query head, give the error of
+        # the fp32-P path on identical data (checked once, not timed).
+        g = hq // hkv
+        kr, vr = (c.repeat_interleave(g, dim=1) for c in (kc, vc))
+        out1 = ak.paged_decode(q, kr, vr, tables, clens, max_ctx, partition_size=part)
+        per_impl["paged_split"]["max_abs_err_one_head_path"] = float(f"{error(out1):.3g}")
+        del kr, vr, out1
     fields = dict(batch=B, ctx=max_ctx, ctx_mean=round(sum(lens) / B, 1), heads=hq, kv_heads=hkv, head_dim=d,
                   block_size=bs, **(extra or {}))
     return Case(section, fields, float(sum(lens)) * hkv * d * 2 * 2, "GB/s", impls, error,

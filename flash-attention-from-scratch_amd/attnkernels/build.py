@@ -33,7 +33,7 @@ LIB = PKG / "libattnkernels.so"
 EXT_NAME = "attnkernels_ext"
 ARCH = os.environ.get("ATTN_OFFLOAD_ARCH", "gfx950")
 
-HIP_SOURCES = ["prefill.hip", "decode.hip", "cache_write.hip"]
+HIP_SOURCES = ["prefill.hip", "decode.hip", "cache_write.hip", "stream.hip"]
 CPP_SOURCES = ["capi.cpp"]
 
 # Packed FP32 VALU ops stay disabled on this pool; hipcc's host pass warns it

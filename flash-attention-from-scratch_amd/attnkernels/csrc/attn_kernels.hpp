@@ -74,5 +74,7 @@ constexpr int64_t kFusedMaxSplits = 32;
 constexpr size_t kDecodeScratchCounters = size_t(1) << 18;
 hipError_t decode_scratch(void** ptr, int32_t** counters);
 hipError_t cache_write_launch(const CacheWriteArgs& a);
+// XOR of the 16-byte words of src (bytes / 16 of them) into out[0..3].
+hipError_t stream_checksum_launch(const void* src, size_t bytes, uint32_t* out, void* stream);
 
 }  // namespace ak

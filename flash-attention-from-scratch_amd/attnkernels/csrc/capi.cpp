@@ -320,4 +320,13 @@ int ak_reshape_and_cache(const void* key, const void* value, void* k_cache, void
     return hip_status(ak::cache_write_launch(a), "reshape_and_cache");
 }
 
+int ak_stream_checksum(const void* src, size_t bytes, uint32_t* out, void* stream) {
+    if (bytes % 16 != 0) return fail(AK_ERR_INVALID_ARGUMENT, "stream_checksum: bytes must be a multiple of 16");
+    if (bytes > 0 && (!src || !aligned16(src)))
+        return fail(AK_ERR_INVALID_ARGUMENT, "stream_checksum: src must be a 16-byte aligned device pointer");
+    if (!out || (reinterpret_cast<uintptr_t>(out) & 3u))
+        return fail(AK_ERR_INVALID_ARGUMENT, "stream_checksum: out must be a 4-byte aligned device pointer");
+    return hip_status(ak::stream_checksum_launch(src, bytes, out, stream), "stream_checksum");
+}
+
 }  // extern "C"

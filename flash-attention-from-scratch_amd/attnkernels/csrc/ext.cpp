@@ -178,12 +178,36 @@ void reshape_and_cache(torch::Tensor key, torch::Tensor value, torch::Tensor kc,
                                   T > 1 ? value.stride(0) : value.size(1) * value.size(2), stream_of(key)));
 }
 
+// XOR checksum of a tensor's bytes (a multiple of 16): the read-only
+// streaming kernel behind bench.py's HBM read ceiling.
+// out (int32[4] on x's device) accumulates the XOR when given: the caller
+// zeroes it; without it a zeroed one is made.
+torch::Tensor stream_checksum(torch::Tensor x, c10::optional<torch::Tensor> out_opt) {
+    TORCH_CHECK(x.is_cuda() && x.is_contiguous() && x.nbytes() % 16 == 0,
+                "stream_checksum: a contiguous GPU tensor of a multiple of 16 bytes");
+    const at::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+    torch::Tensor out;
+    if (out_opt.has_value()) {
+        out = *out_opt;
+        TORCH_CHECK(out.device() == x.device() && out.scalar_type() == torch::kInt && out.numel() == 4 &&
+                        out.is_contiguous(),
+                    "stream_checksum: out must be a contiguous int32[4] on the input's device");
+    } else {
+        out = torch::zeros({4}, x.options().dtype(torch::kInt));
+    }
+    check_rc(ak_stream_checksum(x.data_ptr(), x.nbytes(), reinterpret_cast<uint32_t*>(out.data_ptr<int32_t>()),
+                                stream_of(x)));
+    return out;
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.doc() = "gfx950 attention kernels: MFMA flash prefill, paged split-K decode";
     m.def("naive_attention", &naive_attention, "prefill attention (served by the MFMA flash kernel)");
     m.def("flash_simt", &flash_simt, "prefill attention (served by the MFMA flash kernel)");
     m.def("flash_wmma", &flash_wmma, "tiled attention with online softmax on MFMA matrix cores");
     m.def("paged_decode", &paged_decode, "decode attention over a paged KV cache, split-K");
+    m.def("stream_checksum", &stream_checksum, "XOR checksum of a tensor's bytes (read-only streaming ceiling)",
+          py::arg("x"), py::arg("out") = py::none());
     m.def("reshape_and_cache", &reshape_and_cache, "write new tokens' K/V rows into the paged caches");
     m.def("flash_gqa", &flash_gqa, "dense prefill with grouped-query attention");
     m.def("flash_varlen", &flash_varlen, "prefill over packed variable-length sequences");

@@ -44,6 +44,16 @@ COPY_KERNEL = "__amd_rocclr_copyBuffer"
 CALIB_BYTES = 1 << 30         # bench.py --calib-copy: one plain 1 GiB device-to-device copy
 NUM_XCD, NUM_CU, NUM_SIMD = 8, 256, 1024
 PEAK = {"TFLOP/s": 2500.0, "GB/s": 8000.0}
+# Shortest kernel whose clock is derived from GRBM_GUI_ACTIVE / duration: that
+# counter also counts busy cycles around each dispatch, which inflate the
+# derived clock of short kernels.
+CLOCK_MIN_S = 250e-6
+
+
+def zero_counters(c):
+    """Counters of one kernel's table that read 0 on every pass."""
+    names = {nn for (_, nn) in c}
+    return sorted(n for n in names if all(v == 0 for (_, nn), v in c.items() if nn == n))
 
 
 def short_name(name: str) -> str:
@@ -306,13 +316,26 @@ def counters_summary(workload: str, raw: Path, passes, out_dir: Path = PROFILES)
                  "(GRBM_GUI_ACTIVE / 8 = one XCD's active cycles).", "",
                  "| counter | " + " | ".join(passes) + " |", "|---|" + "---:|" * len(passes)]
         for n in sorted({nn for (_, nn) in c}):
+            if n in zero_counters(c):
+                continue
             lines.append(f"| {n} | " + " | ".join(f"{c[(p, n)]:.4g}" if (p, n) in c else "" for p in passes) + " |")
         gui = (get("GRBM_GUI_ACTIVE") or 0) / NUM_XCD
         d_s = statistics.fmean(dur[k]) if dur[k] else 0.0
+        zero = zero_counters(c)
+        if zero:
+            lines += ["", "Left out of the table: " + ", ".join(zero) + " (read 0 on every timed dispatch"
+                      + ("; SQ_ACTIVE_INST_VMEM = 0 on a kernel that streams its data through vector loads is "
+                         "not a count, so the counter does not count on this GPU" if "SQ_ACTIVE_INST_VMEM" in zero
+                         else "") + ")."]
         lines += ["", "Derived:", ""]
-        if gui and d_s > 2e-5:
+        if gui and d_s >= CLOCK_MIN_S:
             lines.append(f"- kernel duration under the counters {d_s * 1e6:.1f} us; shader clock = GRBM_GUI_ACTIVE / 8 / "
                          f"duration = **{gui / d_s / 1e9:.2f} GHz** (peak engine clock 2.4 GHz)")
+        elif gui and d_s:
+            lines.append(f"- kernel duration under the counters {d_s * 1e6:.1f} us: too short to derive the clock. "
+                         "GRBM_GUI_ACTIVE also counts busy cycles around the dispatch, which a kernel under "
+                         f"{CLOCK_MIN_S * 1e6:.0f} us does not amortise (a 45 us decode kernel read 2.55 GHz, above "
+                         "the 2.4 GHz peak); the ratios below that divide by GRBM_GUI_ACTIVE are lower bounds")
         mb, mi = get("SQ_VALU_MFMA_BUSY_CYCLES"), get("SQ_INSTS_MFMA")
         if mb is not None and gui:
             lines.append(f"- MFMA utilisation (SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD x 1024 SIMDs)) = "

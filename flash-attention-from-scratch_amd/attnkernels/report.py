@@ -90,6 +90,18 @@ def worst_error_table(rows):
     return _table(["path", "impl", "shapes", "worst max abs error"], body) if body else ""
 
 
+def head_group_error_table(rows):
+    """Max-abs error against fp32 per head group: the grouped-query kernels
+    (fp16 P) and the one-head kernel (fp32 P) on the same queries and K/V."""
+    sel = sorted((r for r in rows if r["section"] == "decode_heads" and "max_abs_err" in r),
+                 key=lambda r: (r["head_dim"], r.get("group", 1)))
+    body = [[r["head_dim"], r.get("group", 1), f"{r['batch']} x {r['ctx']}", f"{r['max_abs_err']:.2e}",
+             f"{r['max_abs_err_one_head_path']:.2e}" if "max_abs_err_one_head_path" in r else "(the same kernel)"]
+            for r in sel]
+    return _table(["D", "G", "B x ctx", "max abs error (G-head kernel)", "one-head kernel, same data"],
+                  body) if body else ""
+
+
 def decode_time_table(rows, section="decode"):
     sel = [r for r in rows if r["section"] == section]
     if not sel:
@@ -222,6 +234,10 @@ def render(data):
     t = worst_error_table(rows)
     if t:
         lines += ["", "## Worst error against fp32", "", t]
+    t = head_group_error_table(rows)
+    if t:
+        lines += ["", "## Decode error by head group (fp16 P in the grouped-query kernels, fp32 P in the one-head "
+                  "kernel; the same queries and K/V)", "", t]
     for key in ("failed_sections", "failed_cases"):
         if meta.get(key):
             lines += ["", f"{key.replace('_', ' ').capitalize()}: " + json.dumps(meta[key])]

@@ -158,6 +158,13 @@ int ak_paged_decode_noalloc(const void *q, const void *k_cache, const void *v_ca
                             int64_t max_blocks_per_seq, int64_t max_context_len, double scale,
                             int64_t partition, void *stream);
 
+/* Read-only streaming checksum: XORs the bytes / 16 16-byte words of src into
+ * out[0..3] (uint32, device memory the caller zeroes first).  No counterpart
+ * in the reference's kernels: it is the read ceiling of bench.py's measured
+ * ceilings, as the reference's bench measures a device copy
+ * (bench/bench.py:119-131).  bytes a multiple of 16, src 16-byte aligned. */
+int ak_stream_checksum(const void *src, size_t bytes, uint32_t *out, void *stream);
+
 /* Paged KV-cache writer ("reshape and cache"): appends new tokens' keys and
  * values to the paged cache that ak_paged_decode reads.  No counterpart in the
  * reference, which only reads the cache (attnkernels/csrc/paged_decode.cu:95-96);

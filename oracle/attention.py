@@ -144,11 +144,12 @@ def paged_decode_fp32(q, k_cache, v_cache, block_tables, context_lens, scale=Non
         vv = _as_f32(gather_kv(v_cache, tables[b:b + 1], nb)[0, :, :c])
         kk = np.repeat(kk, g, axis=0)
         vv = np.repeat(vv, g, axis=0)
-        s = np.einsum("hd,hcd->hc", q[b], kk) * np.float32(scale)
+        # batched matrix products (BLAS): [H, c, D] x [H, D, 1] and [H, 1, c] x [H, c, D]
+        s = np.matmul(kk, q[b][:, :, None])[..., 0] * np.float32(scale)
         s -= s.max(axis=-1, keepdims=True)
         p = np.exp(s)
         p /= p.sum(axis=-1, keepdims=True)
-        out[b] = np.einsum("hc,hcd->hd", p, vv)
+        out[b] = np.matmul(p[:, None, :], vv)[:, 0, :]
     return out
 
 

@@ -175,3 +175,12 @@ def test_fused_decode_validates_counters_before_any_hip_call(lib):
     assert b"counters" in lib.ak_last_error()
     assert lib.ak_paged_decode_fused(*args, ctypes.c_void_p(4098), 8, None) == 1
     assert b"counters" in lib.ak_last_error()
+
+
+def test_stream_checksum_validates_before_any_hip_call(lib):
+    lib.ak_stream_checksum.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
+    assert lib.ak_stream_checksum(FAKE, 24, FAKE, None) == 1  # not a multiple of 16 bytes
+    assert b"multiple of 16" in lib.ak_last_error()
+    assert lib.ak_stream_checksum(ctypes.c_void_p(4104), 32, FAKE, None) == 1  # src misaligned
+    assert lib.ak_stream_checksum(FAKE, 32, None, None) == 1  # no output
+    assert lib.ak_stream_checksum(None, 0, FAKE, None) == 0  # nothing to read

@@ -91,3 +91,34 @@ def test_capi_context_beyond_table_capacity(lib, hq, hkv):
     assert torch.isfinite(out).all()
     ref = oracle.paged_decode_fp32(q, kc, vc, bt, np.asarray([512, 300], np.int32))
     assert max_err(out, ref) < TOL[128]
+
+
+@pytest.mark.parametrize("nbytes", [16, 48, (1 << 20) + 16 * 37, 300 << 20])
+def test_stream_checksum_is_the_xor_of_all_words(lib, nbytes):
+    """ak_stream_checksum (the bench's read ceiling) reads every 16-byte word
+    once: its result is the XOR of all words, for buffers inside one grid
+    stride, across the unrolled loop, and with a ragged tail."""
+    lib.ak_stream_checksum.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
+    print(f"stream checksum bytes={nbytes}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(nbytes % 1009)
+    src = torch.randint(-2 ** 31, 2 ** 31 - 1, (nbytes // 4,), generator=g, device="cuda", dtype=torch.int32)
+    out = torch.zeros(4, dtype=torch.int32, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib.ak_stream_checksum(ptr(src), nbytes, ptr(out), stream) == 0, lib.ak_last_error()
+    torch.cuda.synchronize()
+    want = np.bitwise_xor.reduce(src.cpu().numpy().view(np.uint32).reshape(-1, 4), axis=0)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want)
+
+
+def test_stream_checksum_extension_accumulates(ext):
+    """The torch entry point: a fresh result, and XOR-accumulation into a
+    caller's int32[4] (the same buffer read twice leaves it at zero)."""
+    x = torch.randint(-2 ** 31, 2 ** 31 - 1, ((5 << 20) // 4 + 12,), device="cuda", dtype=torch.int32)
+    one = ext.stream_checksum(x)
+    acc = torch.zeros(4, dtype=torch.int32, device="cuda")
+    ext.stream_checksum(x, acc)
+    assert torch.equal(one, acc)
+    ext.stream_checksum(x, acc)
+    assert int(acc.count_nonzero()) == 0
+    with pytest.raises(RuntimeError):
+        ext.stream_checksum(x, torch.zeros(3, dtype=torch.int32, device="cuda"))

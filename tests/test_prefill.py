@@ -174,17 +174,20 @@ def _device_qkv(b, h, n, d, seed):
     return [torch.randn(b, h, n, d, generator=g, device="cuda", dtype=torch.float16) for _ in range(3)]
 
 
-@pytest.mark.parametrize("cfg", [(4, 16, 2048, 64, False), (2, 32, 8192, 128, True),
+@pytest.mark.parametrize("cfg", [(1, 4, 256, 64, False), (4, 16, 2048, 64, False), (2, 32, 8192, 128, True),
                                  (2, 32, 8191, 128, True)],
-                         ids=["cfg2_d64_n2048", "cfg3_d128_n8192_causal", "cfg3_d128_n8191_causal"])
+                         ids=["cfg1_d64_n256", "cfg2_d64_n2048", "cfg3_d128_n8192_causal", "cfg3_d128_n8191_causal"])
 def test_baseline_config_slices(cfg):
-    """Full-size launch; (batch, head) slices at both ends checked against the oracle."""
+    """Full-size launch; (batch, head) slices at both ends checked against the
+    oracle (every slice of the small configuration)."""
     b, h, n, d, causal = cfg
+    print(f"baseline slices B={b} H={h} N={n} D={d} causal={causal}", flush=True)
     q, k, v = _device_qkv(b, h, n, d, seed=11)
     out = ak.flash_attention(q, k, v, causal=causal)
     torch.cuda.synchronize()
     assert torch.isfinite(out).all()
-    for bi, hi in [(0, 0), (b - 1, h - 1)]:
+    pairs = [(bi, hi) for bi in range(b) for hi in range(h)] if b * h <= 8 else [(0, 0), (b - 1, h - 1)]
+    for bi, hi in pairs:
         qs, ks, vs = (t[bi, hi].cpu().numpy() for t in (q, k, v))
         ref = oracle.attention_fp32(qs, ks, vs, causal)
         assert max_err(out[bi, hi], ref) < TOL[d], (bi, hi)

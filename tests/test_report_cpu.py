@@ -26,7 +26,8 @@ def _rows():
                          ms=0.1, tflops=700.0, peak_mem_mb=mem, max_abs_err=err, speedup_vs_sdpa=None))
     for g, gbs in ((1, 6000.0), (8, 4000.0)):
         rows.append(dict(section="decode_heads", impl="paged_split", batch=16, ctx=8192, heads=8 * g, kv_heads=8,
-                         head_dim=128, group=g, partition=512, ms=0.09, gbs=gbs, max_abs_err=2e-5))
+                         head_dim=128, group=g, partition=512, ms=0.09, gbs=gbs, max_abs_err=2e-5 * g,
+                         **(dict(max_abs_err_one_head_path=2e-5) if g > 1 else {})))
     return rows
 
 
@@ -46,7 +47,10 @@ def test_render_synthetic():
     assert "| 128 | 8 | 64 | 8 | 16 | 8192 | 512 | 0.0900 | 4000 | 50.0% |" in md
     assert "| prefill | sdpa_fused | 2 | 9.00e-04 |" in md
     assert "| prefill | flash_attention | 2 | 5.00e-04 |" in md
-    assert "| decode | paged_split | 6 | 2.00e-05 |" in md
+    assert "| decode | paged_split | 6 | 1.60e-04 |" in md
+    # the grouped kernel's error beside the one-head kernel's on the same data
+    assert "| 128 | 8 | 16 x 8192 | 1.60e-04 | 2.00e-05 |" in md
+    assert "| 128 | 1 | 16 x 8192 | 2.00e-05 | (the same kernel) |" in md
 
 
 def test_committed_results_render():
