@@ -142,14 +142,20 @@ int ak_paged_decode_fused(const void *q, const void *k_cache, const void *v_cach
  * that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc).  The split partials live in
  * a static per-GPU device array of AK_PAGED_DECODE_NOALLOC_MAX_BYTES (32 MiB),
- * held until the process ends; the call fails with AK_ERR_WORKSPACE, before
- * any HIP call, when ak_paged_decode_workspace_size() for these sizes exceeds
- * it (e.g. 8 sequences x 32 query heads x 128 splits x D=128 need 17 MB).
- * The call itself calls no hipMalloc/hipFree; its first call on a device looks
- * up that device's array (hipGetSymbolAddress).  All calls on one GPU share the
- * array: calls that overlap on one GPU (other streams, other threads) race.
- * `stream` must belong to the current device.  Arguments, results and errors
- * are otherwise those of ak_paged_decode. */
+ * the split counters in another of 1 MiB; the call fails with
+ * AK_ERR_WORKSPACE, before any HIP call, when ak_paged_decode_workspace_size()
+ * for these sizes exceeds 32 MiB (e.g. 8 sequences x 32 query heads x 128
+ * splits x D=128 need 17 MB).  With more than 262144 (sequence, kv head)
+ * pairs the splits are merged by the reduce kernel instead.
+ * The arrays belong to the library's code object: every process that loads it
+ * holds these 33 MiB on each GPU where any of its kernels has run, until the
+ * process ends, whether or not it calls this entry point.
+ * The call calls no hipMalloc/hipFree; every call looks up the current
+ * device's arrays (hipGetSymbolAddress, not an allocation), so no address
+ * outlives a hipDeviceReset.  All calls on one GPU share the arrays: calls
+ * that overlap on one GPU (other streams, other threads) race.  `stream` must
+ * belong to the current device.  Arguments, results and errors are otherwise
+ * those of ak_paged_decode. */
 #define AK_PAGED_DECODE_NOALLOC_MAX_BYTES ((size_t)32 << 20)
 int ak_paged_decode_noalloc(const void *q, const void *k_cache, const void *v_cache,
                             const int32_t *block_tables, const int32_t *context_lens, void *out,

@@ -6,13 +6,16 @@ Two calls in a row, the second with a smaller input, show that the shared
 static arrays carry nothing from one call into the next.  A call allocates no
 device memory, and one captured in a HIP graph replays bit-identically."""
 import ctypes
+import json
+import subprocess
+import sys
 
 import numpy as np
 import pytest
 import torch
 
 import oracle
-from conftest import PKG_DIR, TOL, max_err
+from conftest import PKG_DIR, ROOT, TOL, max_err
 
 pytestmark = pytest.mark.gpu
 
@@ -138,3 +141,19 @@ def test_noalloc_under_graph_capture_replays_bit_identically(lib):
         assert torch.equal(out, eager)
         assert noalloc(lib, other_dev, other_sizes, other, 256) == 0, lib.ak_last_error()
         torch.cuda.synchronize()
+
+
+def test_noalloc_first_call_on_the_device_inside_a_graph_capture():
+    """In a fresh process, the library's first call on the device is a
+    noalloc call inside a graph capture (the symbol lookup and module load
+    happen under capture); replays equal the fused entry point bit for bit and,
+    after the graph's first launch, leave free device memory unchanged."""
+    helper = ROOT / "tests" / "noalloc_capture_first.py"
+    r = subprocess.run([sys.executable, str(helper)], capture_output=True, text=True, timeout=100)
+    print(r.stdout, r.stderr[-2000:], flush=True)
+    assert r.returncode == 0
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    assert res["capture_rc"] == 0, res["error"]
+    assert res["fused_rc"] == 0 and res["finite"]
+    assert res["replays_equal"] == [True] * 4
+    assert res["free_unchanged"]
