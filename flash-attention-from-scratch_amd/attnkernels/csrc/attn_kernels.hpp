@@ -26,6 +26,11 @@ struct PrefillArgs {
     void* stream;
 };
 
+// Launches of the grouped-query decode kernel with at least this many waves
+// (at 4 per workgroup) keep 4-wave workgroups; smaller grids use 8 waves per
+// workgroup.
+constexpr int64_t kGqaManyWaves = 2048;
+
 struct DecodeArgs {
     const void* q;         // [B, hq, D] fp16
     const void* k_cache;   // [num_blocks, hkv, bs, D] fp16

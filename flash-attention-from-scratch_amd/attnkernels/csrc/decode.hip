@@ -394,9 +394,9 @@ paged_decode_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const
 // register by register at the end (lane permutes, no LDS), and the waves of the
 // workgroup through LDS as above.
 
-template <int D, int G>
+template <int D, int G, int NW_>
 struct GqaTile {
-    static constexpr int NW = 4;                 // waves per workgroup
+    static constexpr int NW = NW_;               // waves per workgroup
     static constexpr int THREADS = NW * kWave;
     static constexpr int LPT = D / 8;            // lanes per token row (a lane group)
     static constexpr int TPL = kWave / LPT;      // tokens per wave-wide load
@@ -483,14 +483,14 @@ __device__ __forceinline__ float across_groups(float x, Op op) {
     return xor_combine<32>(x, op);
 }
 
-template <int D, int G>
-__global__ void __launch_bounds__((GqaTile<D, G>::THREADS))
+template <int D, int G, int NW>
+__global__ void __launch_bounds__((GqaTile<D, G, NW>::THREADS))
 paged_decode_gqa_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const f16* __restrict__ vc,
                         const int* __restrict__ block_tables, const int* __restrict__ ctx_lens,
                         f16* __restrict__ out, float* __restrict__ o_part, float* __restrict__ m_part,
                         float* __restrict__ l_part, int32_t* __restrict__ counters, int hkv, int bs,
                         int bs_shift, int max_blocks, int num_blocks, int partition, int num_splits, float sl2) {
-    using T = GqaTile<D, G>;
+    using T = GqaTile<D, G, NW>;
     constexpr int U = T::U, N = T::N, S = T::S, LB = T::LB;
     // P = 2^(s - m + kPShift): the largest P the fast path accepts is 2^kPMax.
     constexpr float kPShift = 7.f, kPMax = 32768.f;
@@ -806,6 +806,20 @@ paged_reduce_kernel(const float* __restrict__ o_part, const float* __restrict__ 
     }
 }
 
+// Waves per workgroup of the grouped-query kernel.  A wave reads one 16-token
+// page per round trip to memory, so a split of P tokens costs P / (16 NW)
+// dependent round trips; with many workgroups per CU they overlap, but in a
+// small grid (one sequence, few kv heads) they are the kernel's critical path.
+// Measured on MI355X (one call after a 512 MiB flush, G = 2, 4, 8, D = 64 and
+// 128): grids under 512 workgroups run 0.3-1.9 us faster with 8 waves than
+// with 4 (B=1 ctx 1024: 11.8 vs 13.7 us; ctx 16384: 20.8 vs 21.4 us), and 16
+// waves are slower than 8 everywhere; from 512 workgroups up, 4 waves win.
+template <int G>
+static int gqa_waves(const DecodeArgs& a) {
+    const int64_t wgs = a.batch * a.hkv * a.num_splits;
+    return wgs * 4 >= kGqaManyWaves ? 4 : 8;
+}
+
 template <int D, int G>
 static hipError_t launch_decode(const DecodeArgs& a) {
     int bs_shift = -1;
@@ -821,12 +835,20 @@ static hipError_t launch_decode(const DecodeArgs& a) {
                            (const f16*)a.k_cache, (const f16*)a.v_cache, a.block_tables, a.context_lens,
                            (f16*)a.out, a.o_part, a.m_part, a.l_part, counters, (int)a.hkv, (int)a.bs, bs_shift,
                            (int)a.max_blocks, (int)a.num_blocks, (int)a.partition, (int)a.num_splits, a.sl2);
-    else
-        hipLaunchKernelGGL((paged_decode_gqa_kernel<D, G>), grid, dim3(GqaTile<D, G>::THREADS), 0, stream,
-                           (const f16*)a.q, (const f16*)a.k_cache, (const f16*)a.v_cache, a.block_tables,
-                           a.context_lens, (f16*)a.out, a.o_part, a.m_part, a.l_part, counters, (int)a.hkv,
-                           (int)a.bs, bs_shift, (int)a.max_blocks, (int)a.num_blocks, (int)a.partition,
-                           (int)a.num_splits, a.sl2);
+    else {
+        auto launch = [&](auto nw) {
+            constexpr int NW = decltype(nw)::value;
+            hipLaunchKernelGGL((paged_decode_gqa_kernel<D, G, NW>), grid, dim3(GqaTile<D, G, NW>::THREADS), 0,
+                               stream, (const f16*)a.q, (const f16*)a.k_cache, (const f16*)a.v_cache,
+                               a.block_tables, a.context_lens, (f16*)a.out, a.o_part, a.m_part, a.l_part, counters,
+                               (int)a.hkv, (int)a.bs, bs_shift, (int)a.max_blocks, (int)a.num_blocks,
+                               (int)a.partition, (int)a.num_splits, a.sl2);
+        };
+        if (gqa_waves<G>(a) == 8)
+            launch(std::integral_constant<int, 8>{});
+        else
+            launch(std::integral_constant<int, 4>{});
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.num_splits == 1 || counters) return e;
     hipLaunchKernelGGL((paged_reduce_kernel<D>), dim3((unsigned)(a.batch * a.hq)), dim3(256), 0, stream,

@@ -188,3 +188,22 @@ def test_extension_decode_steps_on_one_stream(ext):
                 out = ak.paged_decode(qd, kcd, vcd, btd, cld, max(lens), partition_size=256)
             s.synchronize()
             assert max_err(out, c.oracle()) < TOL[d]
+
+
+@pytest.mark.parametrize("hq,d", [(32, 128), (64, 128), (16, 64)])
+def test_small_and_large_grid_wave_counts_agree(lib, hq, d):
+    """One sequence of 16384 tokens, 8 kv heads: partition 512 gives 256
+    workgroups (the grouped-query kernel's 8-wave workgroups, merged in the
+    kernel), partition 256 gives 512 (4-wave workgroups, merged by the reduce
+    kernel).  Both against the oracle and each other."""
+    print(f"wave counts hq={hq} d={d}", flush=True)
+    c = Case([16384], hq, 8, d, seed=hq + d)
+    ref = c.oracle()
+    outs = []
+    for p in (512, 256):
+        ws, counters = buffers(lib, c, p)
+        outs.append(c.run(lib, p, True, ws, counters))
+        torch.cuda.synchronize()
+        assert int(torch.count_nonzero(counters)) == 0
+        assert max_err(outs[-1], ref) < TOL[d]
+    assert max_err(outs[0], outs[1]) < 1e-3
