@@ -483,7 +483,7 @@ __device__ __forceinline__ float across_groups(float x, Op op) {
     return xor_combine<32>(x, op);
 }
 
-template <int D, int G, int NW>
+template <int D, int G, int NW, bool PIPE>
 __global__ void __launch_bounds__((GqaTile<D, G, NW>::THREADS))
 paged_decode_gqa_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const f16* __restrict__ vc,
                         const int* __restrict__ block_tables, const int* __restrict__ ctx_lens,
@@ -668,9 +668,6 @@ paged_decode_gqa_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, c
     // (prefetched one chunk ahead) and every K/V load is page base + lane
     // offset.  The checked loop takes the rest: the context's tail, an
     // out-of-range page id, and every chunk when pages are not 16 tokens.
-    // (Software-pipelining this loop, the next chunk's K and V issued under
-    // this chunk's work, measured 0-7% slower on MI355X: the loop is not
-    // latency-bound at 3-4 waves per SIMD.)
     int t0 = start + w * T::TOK;
     {
         auto load_kv = [&](const f16* cache, int pid, f16x8 (&r)[U]) {
@@ -680,16 +677,49 @@ paged_decode_gqa_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, c
                 r[u] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(base + lane_off[u]));
         };
         const bool unused[U] = {};
-        while (fast_bs && t0 + T::TOK <= end && (unsigned)spg < (unsigned)num_blocks) {
-            f16x8 kr[U], vr[U];
-            load_kv(kc, spg, kr);
-            load_kv(vc, spg, vr);
-            const int tn = t0 + stride;
-            if (tn + T::TOK <= end) spg = bt[uniform(tn >> 4)];
-            float x[2];
-            scores(kr, x);
-            finish(x, vr, unused, std::false_type{});
-            t0 = tn;
+        if constexpr (PIPE) {
+            // Software-pipelined: chunk t0 + stride's K and V are issued before
+            // chunk t0 is computed (page ids one chunk further ahead), in two
+            // register sets that swap roles every chunk.  A step computes chunk
+            // t0 and returns whether the next chunk was issued; when it was not
+            // (tail, bad page id), t0 is that chunk and the checked loop takes it.
+            auto step = [&](const f16x8 (&kcur)[U], const f16x8 (&vcur)[U], f16x8 (&knext)[U],
+                            f16x8 (&vnext)[U], int& spn) {
+                const int tn = t0 + stride;
+                const bool issued = tn + T::TOK <= end && (unsigned)spn < (unsigned)num_blocks;
+                if (issued) {
+                    load_kv(kc, spn, knext);
+                    load_kv(vc, spn, vnext);
+                    const int tnn = tn + stride;
+                    if (tnn + T::TOK <= end) spn = bt[uniform(tnn >> 4)];
+                }
+                float x[2];
+                scores(kcur, x);
+                finish(x, vcur, unused, std::false_type{});
+                t0 = tn;
+                return issued;
+            };
+            if (fast_bs && t0 + T::TOK <= end && (unsigned)spg < (unsigned)num_blocks) {
+                f16x8 ka[U], va[U], kb[U], vb[U];
+                load_kv(kc, spg, ka);
+                load_kv(vc, spg, va);
+                int spn = -1;
+                if (t0 + stride + T::TOK <= end) spn = bt[uniform((t0 + stride) >> 4)];
+                while (step(ka, va, kb, vb, spn) && step(kb, vb, ka, va, spn)) {
+                }
+            }
+        } else {
+            while (fast_bs && t0 + T::TOK <= end && (unsigned)spg < (unsigned)num_blocks) {
+                f16x8 kr[U], vr[U];
+                load_kv(kc, spg, kr);
+                load_kv(vc, spg, vr);
+                const int tn = t0 + stride;
+                if (tn + T::TOK <= end) spg = bt[uniform(tn >> 4)];
+                float x[2];
+                scores(kr, x);
+                finish(x, vr, unused, std::false_type{});
+                t0 = tn;
+            }
         }
     }
     if (t0 < end) load_pages(t0, end, pg);
@@ -806,6 +836,13 @@ paged_reduce_kernel(const float* __restrict__ o_part, const float* __restrict__ 
     }
 }
 
+// Software pipelining of the grouped-query kernel's main loop (the next
+// chunk's K and V issued before this chunk is computed).  Measured on MI355X,
+// back-to-back calls at the default partition: D = 64 with 4 and 8 query heads
+// per kv head +4% to +6.5%; D = 128 -2% to +3% (G = 8: -1.5% to +2.9%), so
+// only D = 64 pipelines.
+constexpr bool gqa_pipelined(int d, int g) { return d == 64 && g >= 4; }
+
 // Waves per workgroup of the grouped-query kernel.  A wave reads one 16-token
 // page per round trip to memory, so a split of P tokens costs P / (16 NW)
 // dependent round trips; with many workgroups per CU they overlap, but in a
@@ -838,7 +875,8 @@ static hipError_t launch_decode(const DecodeArgs& a) {
     else {
         auto launch = [&](auto nw) {
             constexpr int NW = decltype(nw)::value;
-            hipLaunchKernelGGL((paged_decode_gqa_kernel<D, G, NW>), grid, dim3(GqaTile<D, G, NW>::THREADS), 0,
+            hipLaunchKernelGGL((paged_decode_gqa_kernel<D, G, NW, gqa_pipelined(D, G)>), grid,
+                               dim3(GqaTile<D, G, NW>::THREADS), 0,
                                stream, (const f16*)a.q, (const f16*)a.k_cache, (const f16*)a.v_cache,
                                a.block_tables, a.context_lens, (f16*)a.out, a.o_part, a.m_part, a.l_part, counters,
                                (int)a.hkv, (int)a.bs, bs_shift, (int)a.max_blocks, (int)a.num_blocks,
