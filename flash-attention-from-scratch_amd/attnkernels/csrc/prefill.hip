@@ -19,8 +19,8 @@
 //     at two waves per SIMD sustains 1.9-2.0 PFLOP/s on random fp16 data
 //     against 1.2-1.6 for 32x32, and the D = 128 kernel runs at a 12% higher
 //     clock with it.  It also issues twice the MFMA instructions, so it pays
-//     only where the key loop is long: D = 128 with 8-wave workgroups and
-//     N >= 6144.
+//     only where the key loop is long: D = 128 with 8-wave workgroups, causal
+//     N >= 6144 and non-causal N >= 3072.
 //   * Scores are computed transposed, S^T = K Q^T, with K as the MFMA A operand
 //     (16-byte LDS reads of K rows) and Q as the B operand (kept in VGPRs for
 //     the whole kernel).
@@ -168,9 +168,14 @@ __device__ __forceinline__ int v_chunk(int r, int c) {
 // tile's first row) plus a 32-bit per-lane offset that is the same for every
 // tile, so the address arithmetic is scalar; only a tile that crosses n takes
 // the clamped per-lane 64-bit addresses.  Both issue LPW loads per wave.
-// Measured on MI355X: non-causal N = 8192 +5%, causal N = 2048-8192 +0.4% to
-// +2%; at D = 64 no gain, and the causal varlen kernel loses its third wave
-// per SIMD to the extra registers, so D = 64 keeps the per-lane addresses.
+// The branch splits a tile body into scheduling regions: the compiler then
+// issues V(t+1) right after the next tile's QK^T MFMAs and this tile's
+// exponentials after it, instead of interleaving them with those MFMAs.
+// Measured on MI355X against per-lane addresses: non-causal N = 8192 +4-5%,
+// causal N = 2048-8192 +0.4% to +2%; against the same scalar loads with the
+// clamp folded into the offset (no branch, interleave kept) +1% to +4% at
+// N >= 4096.  At D = 64 no gain, and the causal varlen kernel loses its third
+// wave per SIMD to the extra registers, so D = 64 keeps the per-lane addresses.
 template <int D, bool IS_V, int NW, int M>
 __device__ __forceinline__ void load_kv(const f16* __restrict__ src, f16* dst, int k0, int n, int rs, int w,
                                         int lane) {
@@ -874,18 +879,21 @@ static int prefill_waves(int64_t n, bool causal, int64_t bh) {
 
 // MFMA shape.  16x16x32 where the key loop is long enough for its lower energy
 // per FLOP (a higher clock under the power limit) to outweigh its twice as
-// many MFMA issues: D = 128, 8-wave workgroups, N >= 6144.  Measured against
-// 32x32x16 on one box at a time: causal N = 8192 +1% to +4%, non-causal +3% to
-// +4.4%; causal N = 4096 -6% to +1%, N = 2048 -4% to -7%, the 4-wave kernels
-// -6% to -9%, and D = 64 -3% to -11% (its two exponentials per 32x32 MFMA
-// leave no issue slots for the extra MFMA instructions).
-static bool prefill_mfma16(int64_t n, int d, int nw) { return d == 128 && nw == 8 && n >= 6144; }
+// many MFMA issues: D = 128, 8-wave workgroups, causal N >= 6144, non-causal
+// N >= 3072.  Measured against 32x32x16 on one box at a time: causal N = 8192
+// +0% to +4%, non-causal N = 4096 +4.5% to +6.7%, N = 3072 +1%, N = 2048 even;
+// causal N = 3072-4096 -4% to -7%, the 4-wave kernels -6% to -9%, and D = 64
+// -3% to -11% (its two exponentials per 32x32 MFMA leave no issue slots for
+// the extra MFMA instructions).
+static bool prefill_mfma16(int64_t n, int d, int nw, bool causal) {
+    return d == 128 && nw == 8 && n >= (causal ? 6144 : 3072);
+}
 
 template <int D, bool CAUSAL>
 static hipError_t launch_prefill(const PrefillArgs& a) {
     if (prefill_waves(a.n, CAUSAL, a.bh) == 4) return launch_prefill_nw<D, CAUSAL, 4, 32>(a);
     if constexpr (D == 128) {
-        if (prefill_mfma16(a.n, D, 8)) return launch_prefill_nw<D, CAUSAL, 8, 16>(a);
+        if (prefill_mfma16(a.n, D, 8, CAUSAL)) return launch_prefill_nw<D, CAUSAL, 8, 16>(a);
     }
     return launch_prefill_nw<D, CAUSAL, 8, 32>(a);
 }

@@ -96,6 +96,21 @@ def test_running_max_moves_late(causal, b, h, n, d):
         assert max_err(out[:, hi], ref) < 2 * TOL[d], hi
 
 
+@pytest.mark.parametrize("causal,h,n", [(False, 16, 3071), (False, 16, 3072), (False, 12, 4100), (True, 16, 6143),
+                                        (True, 16, 6144)])
+def test_mfma_shape_boundaries(causal, h, n):
+    """D = 128 on 8-wave workgroups either side of the switch from 32x32x16 to
+    16x16x32 MFMAs (non-causal at N = 3072, causal at N = 6144), ragged and
+    whole key tiles: first and last head against the oracle."""
+    print(f"mfma shape boundary causal={causal} h={h} n={n}", flush=True)
+    q, k, v = rand_qkv(1, h, n, 128, seed=n)
+    out = run("wmma64", q, k, v, causal)
+    assert torch.isfinite(out).all()
+    for hi in (0, h - 1):
+        ref = oracle.attention_fp32(q[:, hi].numpy(), k[:, hi].numpy(), v[:, hi].numpy(), causal)
+        assert max_err(out[:, hi], ref) < TOL[128], hi
+
+
 def test_causal_first_row_is_v0():
     q, k, v = rand_qkv(1, 1, 128, 64, seed=5)
     for name in VARIANTS:
