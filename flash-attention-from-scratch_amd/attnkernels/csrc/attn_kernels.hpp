@@ -75,7 +75,7 @@ constexpr size_t kDecodeScratchBytes = size_t(32) << 20;
 // Hq = 32, Hkv = 8: 8-16 splits merged in the kernel save 1.5 us a call, 32
 // break even, 64 lose 3 us).
 constexpr int64_t kFusedMaxSplits = 32;
-// Split counters of the static per-GPU array (sequences x query heads).
+// Split counters of the static per-GPU array: one per (sequence, kv head).
 constexpr size_t kDecodeScratchCounters = size_t(1) << 18;
 hipError_t decode_scratch(void** ptr, int32_t** counters);
 hipError_t cache_write_launch(const CacheWriteArgs& a);

@@ -40,11 +40,13 @@ void* stream_of(const torch::Tensor& t) {
 // counters at zero, so the calls on a stream (which run in order) share it.
 // A stream that needs more counters gets a new, larger array; the smaller one
 // is kept, because a captured graph may still use it.
+// The cache is never destroyed: its tensors would otherwise be freed during
+// static destruction, after torch's allocator or the HIP runtime may be gone.
 torch::Tensor split_counters(const torch::Tensor& q, int64_t n) {
     static std::mutex mu;
-    static std::map<std::pair<int, void*>, std::vector<torch::Tensor>> cache;
+    static auto* cache = new std::map<std::pair<int, void*>, std::vector<torch::Tensor>>();
     std::lock_guard<std::mutex> lock(mu);
-    auto& arrays = cache[{(int)q.device().index(), stream_of(q)}];
+    auto& arrays = (*cache)[{(int)q.device().index(), stream_of(q)}];
     if (arrays.empty() || arrays.back().numel() < n) {
         const int64_t grow = arrays.empty() ? 0 : 2 * arrays.back().numel();
         arrays.push_back(torch::zeros({std::max(n, std::max<int64_t>(grow, 4096))}, q.options().dtype(torch::kInt)));

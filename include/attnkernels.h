@@ -127,7 +127,7 @@ int ak_paged_decode(const void *q, const void *k_cache, const void *v_cache,
  *                 them zero, so one array serves any later call on the same
  *                 stream (calls that share it must not overlap).  NULL: the
  *                 reduce kernel merges, exactly as ak_paged_decode.
- * Launches with more than 64 splits merge in the reduce kernel either way
+ * Launches with more than 32 splits merge in the reduce kernel either way
  * (its workgroups per row read the partials in parallel).  Arguments, results
  * and errors are otherwise those of ak_paged_decode. */
 int ak_paged_decode_fused(const void *q, const void *k_cache, const void *v_cache,

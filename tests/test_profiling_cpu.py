@@ -100,3 +100,46 @@ def test_bench_args_of_input_patterns():
     assert profiling.bench_args("decode_gqa16_d128") == "--only decode_gqa16_d128"
     assert profiling.bench_args("prefill_d128_n8192_causal_zeros") == "--only prefill_d128_n8192_causal --inputs zeros"
     assert profiling.bench_args("prefill_d64_n2048_signs") == "--only prefill_d64_n2048 --inputs signs"
+
+
+CTR_HEADER = ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value", "Start_Timestamp", "End_Timestamp",
+              "Workgroup_Size"]
+PRE = "void ak::flash_prefill_kernel<128, true, false, 8, 16>(_Float16 const*, int)"
+CEIL = "ak::stream_checksum_kernel(unsigned int __vector(4) const*, unsigned long, unsigned long, unsigned int*)"
+
+
+def test_counters_summary_rules(tmp_path):
+    """Counters that read 0 on every timed dispatch are listed, not tabled;
+    the clock is derived only for kernels of 250 us or more (a 50 us kernel
+    whose GRBM_GUI_ACTIVE implies 2.55 GHz gets no clock line); bench.py's
+    read-ceiling kernel gets no summary."""
+    raw = tmp_path / "raw"
+    raw.mkdir()
+    n0, K = 2, 3
+    kernels = {DEC: (50_000, 2.55e9), PRE: (1_000_000, 2.0e9), CEIL: (300_000, 2.4e9)}
+    passes = {"ctr1": ("GRBM_GUI_ACTIVE", "SQ_WAVE_CYCLES", "SQ_ACTIVE_INST_VMEM"),
+              "ctr2": ("GRBM_GUI_ACTIVE", "SQ_WAIT_ANY")}
+    for p, names in passes.items():
+        rows, did, t = [], 0, 0
+        for _ in range(n0 + K):
+            for name, (dur_ns, clock) in kernels.items():
+                did += 1
+                for c in names:
+                    v = {"GRBM_GUI_ACTIVE": 8 * clock * dur_ns * 1e-9, "SQ_WAVE_CYCLES": 1e6,
+                         "SQ_ACTIVE_INST_VMEM": 0.0, "SQ_WAIT_ANY": 3e5}[c]
+                    rows.append([did, name, c, v, t, t + dur_ns, 256])
+                t += dur_ns + 1000
+        with open(raw / f"{p}_counter_collection.csv", "w", newline="") as f:
+            w = csv.writer(f)
+            w.writerow(CTR_HEADER)
+            w.writerows(rows)
+        (raw / f"bench_{p}.json").write_text(json.dumps({"workloads": [{"name": "w", "calls_before_timed": n0}],
+                                                          "steps": K, "sources_sha256": "0" * 64}) + "\n")
+    out_dir = tmp_path / "profiles"
+    out_dir.mkdir()
+    outs = {o.name: o.read_text() for o in profiling.counters_summary("w", raw, list(passes), out_dir)}
+    assert set(outs) == {"paged_decode_kernel_w_counters.md", "flash_prefill_kernel_w_counters.md"}
+    dec, pre = outs["paged_decode_kernel_w_counters.md"], outs["flash_prefill_kernel_w_counters.md"]
+    assert "Left out of the table: SQ_ACTIVE_INST_VMEM" in dec and "| SQ_ACTIVE_INST_VMEM |" not in dec
+    assert "too short to derive the clock" in dec and "GHz**" not in dec
+    assert "**2.00 GHz**" in pre and "too short" not in pre
