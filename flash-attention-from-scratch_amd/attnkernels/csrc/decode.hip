@@ -9,19 +9,22 @@
 // reduce merges partials with M = max m_s, w_s = l_s 2^(m_s - M),
 // O = sum w_s o_s / sum w_s.
 //
-// Both kernels are built for HBM bandwidth, with no matrix cores:
-//   * a token row of one page is D*2 contiguous bytes; D/8 lanes (a lane
-//     group) cover it with one 16-byte load each, so one wave-wide load reads 4
-//     (D=128) or 8 (D=64) tokens = 1 KB;
-//   * the dot products are v_dot2_f32_f16 on the raw fp16 q and k, scaled by
+// The kernels are built for HBM bandwidth:
+//   * in the dot-product kernels a token row of one page (D*2 contiguous
+//     bytes) is covered by D/8 lanes (a lane group) with one 16-byte load each,
+//     so one wave-wide load reads 4 (D=128) or 8 (D=64) tokens = 1 KB;
+//   * their dot products are v_dot2_f32_f16 on the raw fp16 q and k, scaled by
 //     scale*log2(e) in fp32 afterwards;
 //   * with one query head per kv head (paged_decode_kernel) a D=128 lane keeps
 //     16 K loads and 16 V loads in flight, a D=64 lane 4 and 4; each lane
 //     group reduces its dot products with a DPP tree and runs its own online
 //     softmax over the tokens it loads;
-//   * with head groups (paged_decode_gqa_kernel, below) the arithmetic per
-//     byte grows G-fold, and the lane groups share the reduction, the
-//     exponentials and P V out by a butterfly (see there);
+//   * with two or four heads per kv head (paged_decode_gqa_kernel, below)
+//     the arithmetic per byte grows G-fold, and the lane groups share the
+//     reduction, the exponentials and P V out by a butterfly (see there);
+//   * with eight (paged_decode_gqa_mfma_kernel) both products run on the
+//     matrix cores, 16x16x32 MFMAs over page pairs, with the K and V loads laid
+//     out as the MFMA operands (see there);
 //   * the lane groups of a wave and the waves of a workgroup are merged once,
 //     at the end, by the same LSE rule.
 #include "attn_kernels.hpp"
@@ -365,7 +368,8 @@ paged_decode_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const
 }
 
 // ---------------------------------------------------------------------------
-// Grouped-query decode: G = 2, 4 or 8 query heads per kv head.
+// Grouped-query decode on dot products: G = 2 or 4 query heads per kv head
+// (eight go to the matrix-core kernel further below).
 //
 // The kernel above, given head groups, runs out of VALU issue before HBM: each
 // (head, token) dot product is reduced over its D/8 lanes by a DPP tree, every
@@ -408,7 +412,7 @@ struct GqaTile {
     static constexpr int S = LB < LOGN - 1 ? LB : LOGN - 1;  // stages that scatter
     static constexpr int HB = G == 2 ? 1 : G == 4 ? 2 : 3;   // head bits of a value index
     static_assert(D == 128 || D == 64, "head dim");
-    static_assert(G == 2 || G == 4 || G == 8, "head group");
+    static_assert(G == 2 || G == 4, "head group");
     static_assert((N >> S) == 2, "two scores per lane after the scatter");
     static_assert(S >= HB, "the scatter resolves every head bit");
 };
@@ -770,6 +774,267 @@ paged_decode_gqa_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, c
                                 hkv, split, num_splits, splits_with_tokens(ctx, partition, num_splits), tid);
 }
 
+// Eight query heads per kv head on the matrix cores
+// (paged_decode_gqa_mfma_kernel).  A wave takes two 16-token pages per
+// iteration and runs both products on v_mfma_f32_16x16x32_f16, the head group
+// padded to the MFMA's 16 rows (rows G..15 hold zeros or values nobody reads):
+//   * S^T = K Q^T per page: A = K (lane l: token l%16 of the page, head dims
+//     32s + 8(l/16) .. +7 for step s < D/32, one 16-byte load each), B = Q^T
+//     (lane l: query head l%16, the same dims, loaded once), so lane
+//     (n = l%16, g = l/16) ends with the raw scores of head n, tokens
+//     4g .. 4g+3 of the page;
+//   * O += P V per page pair, k = 32 tokens: A = P (lane (n, g): head n, the
+//     8 tokens 4g .. 4g+3 of both pages: exactly the scores the lane holds),
+//     B = V, where column n stands for head dims DPL n + j in the j-th of
+//     DPL = D/16 products: the lane loads its 8 tokens' DPL dims (16 or 8
+//     bytes each; one load instruction reads 4 whole token rows) and regroups
+//     them per dim with v_perm; accumulator j then holds heads 4g + r, dim
+//     DPL n + j;
+//   * softmax as in the dot-product kernel: one exponential per score against
+//     a per-head reference max (the same in the head's four lanes) that moves
+//     only when a score exceeds it by more than 8 (base 2), so that fp16
+//     P = 2^(s - m + 7) stays below 2^15; l sums the fp16 P values.
+// The VALU work per page is the V regrouping and the softmax, about 40
+// instructions against about 300 for eight heads on dot products.  Measured
+// on MI355X against the dot-product kernel at the default partition (calls
+// back to back / after a 512 MiB flush): G = 8, B = 8 x 8192 tokens, D = 128
+// +3% / +3%, D = 64 +5-8% / +4-8%; B = 1 x 1024 tokens +3% / +15%.  With
+// two or four heads per kv head it is no faster (-5% to +1%: B = 1-4, 4096-
+// 16384 tokens lose 4-5% back to back), so those keep the dot products.
+template <int D, int G, int NW_>
+struct GqaMfmaTile {
+    static constexpr int NW = NW_;         // waves per workgroup
+    static constexpr int THREADS = NW * kWave;
+    static constexpr int KS = D / 32;      // S^T = K Q^T steps of 32 head dims
+    static constexpr int DPL = D / 16;     // head dims of a V row per lane = P V products per page pair
+    static constexpr int TOK = 32;         // tokens per wave iteration: two 16-token pages
+    static_assert(D == 128 || D == 64, "head dim");
+    static_assert(G >= 2 && G <= 16, "head group within the MFMA's 16 rows");
+};
+
+// At most 168 VGPRs (amdgpu_waves_per_eu(3)), so that three waves share a
+// SIMD (the compiler otherwise moves the accumulators to AGPRs and holds 172
+// registers, two waves); a 128-register bound spills at D = 128.
+template <int D, int G, int NW>
+__global__ void __launch_bounds__((GqaMfmaTile<D, G, NW>::THREADS)) __attribute__((amdgpu_waves_per_eu(3)))
+paged_decode_gqa_mfma_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const f16* __restrict__ vc,
+                             const int* __restrict__ block_tables, const int* __restrict__ ctx_lens,
+                             f16* __restrict__ out, float* __restrict__ o_part, float* __restrict__ m_part,
+                             float* __restrict__ l_part, int32_t* __restrict__ counters, int hkv, int bs,
+                             int bs_shift, int max_blocks, int num_blocks, int partition, int num_splits,
+                             float sl2) {
+    using T = GqaMfmaTile<D, G, NW>;
+    constexpr int KS = T::KS, DPL = T::DPL;
+    typedef _Float16 vrow_t __attribute__((ext_vector_type(DPL)));
+    typedef uint32_t vrow_u __attribute__((ext_vector_type(DPL / 2)));
+    constexpr float kPShift = 7.f, kPMax = 32768.f;
+    __shared__ float red_acc[NW][G][D];
+    __shared__ float red_m[NW][G], red_l[NW][G];
+
+    const int kvh = blockIdx.x, split = blockIdx.y, b = blockIdx.z;
+    const int hq = hkv * G;
+    const int start = split * partition;
+    const int tid = threadIdx.x, lane = tid & 63, w = uniform(tid >> 6);
+    const int n = lane & 15, g = lane >> 4;
+    const int* bt = block_tables + (size_t)b * max_blocks;
+    const int max_tok = max_blocks * bs;
+    const int ctx_raw = ctx_lens[b];
+
+    // Q^T fragments: head n (zeros for n >= G), dims 32 s + 8 g .. +7.
+    f16x8 qf[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qf[s] = f16x8{};
+    if (n < G) {
+        const f16* qrow = q + ((size_t)b * hq + kvh * G + n) * D + 8 * g;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) qf[s] = *reinterpret_cast<const f16x8*>(qrow + 32 * s);
+    }
+    const int stride = NW * T::TOK;
+    const bool fast_bs = bs == 16;
+    int t0 = start + w * T::TOK;
+    int spa = -1, spb = -1;  // page ids of the pair at t0 (wave-uniform), loaded one pair ahead
+    if (fast_bs && t0 + T::TOK <= min(start + partition, max_tok)) {
+        spa = bt[uniform(t0 >> 4)];
+        spb = bt[uniform((t0 >> 4) + 1)];
+    }
+
+    const int ctx = min(ctx_raw, max_tok);
+    if (start >= ctx) {
+        if (num_splits == 1 || (counters && split == 0))
+            for (int idx = tid; idx < G * D; idx += T::THREADS)
+                out[((size_t)b * hq + kvh * G + idx / D) * D + idx % D] = (f16)0.f;
+        return;
+    }
+    const int end = min(ctx, start + partition);
+
+    // Reference max of head n (the same in the head's four lanes), this
+    // lane's share of l for head n, and acc[j][r]: head 4g + r, dim DPL n + j.
+    float m_own = -INFINITY, l_own = 0.f;
+    f32x4 acc[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // One page pair: scores, online softmax and P V.  Score i of the lane is
+    // token 4g + i of page A (i < 4) or 4g + i - 4 of page B, the tokens of V
+    // rows va[i] / vb[i - 4]; tokens with !valid[i] drop out when MASKED.
+    auto step = [&](const f16x8 (&ka)[KS], const f16x8 (&kb)[KS], const vrow_t (&va)[4], const vrow_t (&vb)[4],
+                    const bool (&valid)[8], auto masked) {
+        constexpr bool MASKED = decltype(masked)::value;
+        f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            sa = mfma16x16x32(ka[s], qf[s], sa);
+            sb = mfma16x16x32(kb[s], qf[s], sb);
+        }
+        const float x[8] = {sa[0], sa[1], sa[2], sa[3], sb[0], sb[1], sb[2], sb[3]};
+        float p[8];
+        float bias = kPShift - m_own;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) p[i] = exp2_fast(!MASKED || valid[i] ? fmaf(x[i], sl2, bias) : -INFINITY);
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ok = ok && p[i] <= kPMax;  // false for inf and NaN
+        if (__builtin_amdgcn_ballot_w64(!ok)) {
+            // Move every head's reference max to its running max (first
+            // pair: m = -inf; later: a score above m + 8).  The padding heads
+            // (n >= G, scores 0) move once, on the first pair, like the rest.
+            auto fmax2 = [](float u, float v) { return fmaxf(u, v); };
+            float mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) mx = fmaxf(mx, !MASKED || valid[i] ? x[i] * sl2 : -INFINITY);
+            mx = xor_combine<16>(mx, fmax2);
+            mx = xor_combine<32>(mx, fmax2);
+            const float m_new = fmaxf(m_own, mx);
+            const float m_use = m_new == -INFINITY ? 0.f : m_new;
+            const float alpha = exp2_fast(m_own - m_use);  // 0 while m was -inf
+            l_own *= alpha;
+            m_own = m_new;
+            // accumulator row r is head 4g + r, whose alpha lane 4g + r holds
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float al = __shfl(alpha, 4 * g + r, kWave);
+#pragma unroll
+                for (int j = 0; j < DPL; ++j) acc[j][r] *= al;
+            }
+            bias = kPShift - m_use;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) p[i] = exp2_fast(!MASKED || valid[i] ? fmaf(x[i], sl2, bias) : -INFINITY);
+        }
+        f16x8 pa;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const f16x2 pk = {(f16)p[2 * k], (f16)p[2 * k + 1]};
+            l_own = __builtin_amdgcn_fdot2(pk, f16x2{(f16)1.f, (f16)1.f}, l_own, false);
+            pa[2 * k] = pk[0];
+            pa[2 * k + 1] = pk[1];
+        }
+        // V fragment j: the 8 tokens' dim DPL n + j, two tokens per register.
+        vrow_u vu[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            vu[i] = __builtin_bit_cast(vrow_u, va[i]);
+            vu[i + 4] = __builtin_bit_cast(vrow_u, vb[i]);
+        }
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) {
+            const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+            u32x4 f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) f[k] = __builtin_amdgcn_perm(vu[2 * k + 1][j >> 1], vu[2 * k][j >> 1], sel);
+            acc[j] = mfma16x16x32(pa, __builtin_bit_cast(f16x8, f), acc[j]);
+        }
+    };
+
+    const size_t page_stride = (size_t)hkv * bs * D;  // elements
+    // Whole pairs of 16-token pages: two wave-uniform page ids (loaded one
+    // pair ahead), every K/V load at page base + lane offset.
+    {
+        const uint32_t kv_off = (uint32_t)(kvh * 16 * D);
+        uint32_t koff[KS], voff[4];  // byte offsets inside a page
+#pragma unroll
+        for (int s = 0; s < KS; ++s) koff[s] = (kv_off + n * D + 32 * s + 8 * g) * 2;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) voff[r] = (kv_off + (4 * g + r) * D + DPL * n) * 2;
+        const bool unused[8] = {};
+        while (fast_bs && t0 + T::TOK <= end && (unsigned)spa < (unsigned)num_blocks &&
+               (unsigned)spb < (unsigned)num_blocks) {
+            f16x8 ka[KS], kb[KS];
+            vrow_t va[4], vb[4];
+            const char* kpa = reinterpret_cast<const char*>(kc + (size_t)spa * page_stride);
+            const char* kpb = reinterpret_cast<const char*>(kc + (size_t)spb * page_stride);
+            const char* vpa = reinterpret_cast<const char*>(vc + (size_t)spa * page_stride);
+            const char* vpb = reinterpret_cast<const char*>(vc + (size_t)spb * page_stride);
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {  // streamed once: non-temporal
+                ka[s] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(kpa + koff[s]));
+                kb[s] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(kpb + koff[s]));
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                va[r] = __builtin_nontemporal_load(reinterpret_cast<const vrow_t*>(vpa + voff[r]));
+                vb[r] = __builtin_nontemporal_load(reinterpret_cast<const vrow_t*>(vpb + voff[r]));
+            }
+            const int tn = t0 + stride;
+            if (tn + T::TOK <= end) {
+                spa = bt[uniform(tn >> 4)];
+                spb = bt[uniform((tn >> 4) + 1)];
+            }
+            step(ka, kb, va, vb, unused, std::false_type{});
+            t0 = tn;
+        }
+    }
+    // The rest (context tail, out-of-range page ids, pages not of 16 tokens):
+    // every token row located on its own; rows that are not read are zeros.
+    for (; t0 < end; t0 += stride) {
+        auto locate = [&](int t, bool& ok) -> size_t {  // element offset of token t's row
+            const int pi = bs_shift >= 0 ? (t >> bs_shift) : (t / bs);
+            const int po = bs_shift >= 0 ? (t & (bs - 1)) : (t % bs);
+            const int pid = t < end ? bt[pi] : -1;
+            ok = t < end && (unsigned)pid < (unsigned)num_blocks;
+            return ok ? (size_t)pid * page_stride + ((size_t)kvh * bs + po) * D : 0;
+        };
+        f16x8 ka[KS], kb[KS];
+        vrow_t va[4], vb[4];
+        bool valid[8], kok;
+        const size_t kao = locate(t0 + n, kok);
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+            ka[s] = kok ? *reinterpret_cast<const f16x8*>(kc + kao + 32 * s + 8 * g) : f16x8{};
+        const size_t kbo = locate(t0 + 16 + n, kok);
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+            kb[s] = kok ? *reinterpret_cast<const f16x8*>(kc + kbo + 32 * s + 8 * g) : f16x8{};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const size_t oa = locate(t0 + 4 * g + r, valid[r]);
+            va[r] = valid[r] ? *reinterpret_cast<const vrow_t*>(vc + oa + DPL * n) : vrow_t{};
+            const size_t ob = locate(t0 + 16 + 4 * g + r, valid[r + 4]);
+            vb[r] = valid[r + 4] ? *reinterpret_cast<const vrow_t*>(vc + ob + DPL * n) : vrow_t{};
+        }
+        step(ka, kb, va, vb, valid, std::true_type{});
+    }
+
+    // Merge the wave: l over the four lanes of each head, then the G heads'
+    // rows to LDS for the workgroup's merge.
+    auto add2 = [](float u, float v) { return u + v; };
+    l_own = xor_combine<16>(l_own, add2);
+    l_own = xor_combine<32>(l_own, add2);
+    if (g == 0 && n < G) {
+        red_m[w][n] = m_own;
+        red_l[w][n] = l_own;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int h = 4 * g + r;
+        if (h < G)
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) red_acc[w][h][DPL * n + j] = acc[j][r];
+    }
+    __syncthreads();
+    split_epilogue<D, G, NW>(red_acc, red_m, red_l, 1.f / 128.f, out, o_part, m_part, l_part, counters, b, kvh,
+                             hkv, split, num_splits, splits_with_tokens(ctx, partition, num_splits), tid);
+}
+
 // LSE merge of the split partials (paged_decode.cu:204-215): one 256-thread
 // workgroup per (sequence, query head) row; ns = ceil(ctx/P) partials are
 // merged, with ctx clamped to the table row's capacity max_tok exactly as the
@@ -836,21 +1101,25 @@ paged_reduce_kernel(const float* __restrict__ o_part, const float* __restrict__ 
     }
 }
 
-// Software pipelining of the grouped-query kernel's main loop (the next
-// chunk's K and V issued before this chunk is computed).  Measured on MI355X,
-// back-to-back calls at the default partition: D = 64 with 4 and 8 query heads
-// per kv head +4% to +6.5%; D = 128 -2% to +3% (G = 8: -1.5% to +2.9%), so
-// only D = 64 pipelines.
+// Software pipelining of the dot-product grouped-query kernel's main loop (the
+// next chunk's K and V issued before this chunk is computed).  Measured on
+// MI355X, back-to-back calls at the default partition: D = 64 with 4 query
+// heads per kv head +4% to +6.5%; D = 128 -2% to +3%, so only D = 64 with
+// four heads pipelines.  (The matrix-core kernel for eight heads gains nothing
+// from it: -1% to +1%.)
 constexpr bool gqa_pipelined(int d, int g) { return d == 64 && g >= 4; }
 
-// Waves per workgroup of the grouped-query kernel.  A wave reads one 16-token
-// page per round trip to memory, so a split of P tokens costs P / (16 NW)
-// dependent round trips; with many workgroups per CU they overlap, but in a
-// small grid (one sequence, few kv heads) they are the kernel's critical path.
-// Measured on MI355X (one call after a 512 MiB flush, G = 2, 4, 8, D = 64 and
-// 128): grids under 512 workgroups run 0.3-1.9 us faster with 8 waves than
-// with 4 (B=1 ctx 1024: 11.8 vs 13.7 us; ctx 16384: 20.8 vs 21.4 us), and 16
-// waves are slower than 8 everywhere; from 512 workgroups up, 4 waves win.
+// Waves per workgroup of both grouped-query kernels.  A dot-product wave
+// reads one 16-token page per round trip to memory, so a split of P tokens
+// costs P / (16 NW) dependent round trips; with many workgroups per CU they
+// overlap, but in a small grid (one sequence, few kv heads) they are the
+// kernel's critical path.  Measured on MI355X (one call after a 512 MiB flush,
+// G = 2, 4, 8, D = 64 and 128): grids under 512 workgroups run 0.3-1.9 us
+// faster with 8 waves than with 4 (B=1 ctx 1024: 11.8 vs 13.7 us; ctx 16384:
+// 20.8 vs 21.4 us), and 16 waves are slower than 8 everywhere; from 512
+// workgroups up, 4 waves win.  The matrix-core kernel (two pages per round
+// trip) measured the same way picks the same: 4 waves at B = 8 x 8192 tokens
+// (8 waves -2%), 8 at B = 1 (equal or better).
 template <int G>
 static int gqa_waves(const DecodeArgs& a) {
     const int64_t wgs = a.batch * a.hkv * a.num_splits;
@@ -882,10 +1151,24 @@ static hipError_t launch_decode(const DecodeArgs& a) {
                                (int)a.hkv, (int)a.bs, bs_shift, (int)a.max_blocks, (int)a.num_blocks,
                                (int)a.partition, (int)a.num_splits, a.sl2);
         };
-        if (gqa_waves<G>(a) == 8)
-            launch(std::integral_constant<int, 8>{});
-        else
+        auto launch_mfma = [&](auto nw) {
+            constexpr int NW = decltype(nw)::value;
+            hipLaunchKernelGGL((paged_decode_gqa_mfma_kernel<D, G, NW>), grid, dim3(GqaMfmaTile<D, G, NW>::THREADS),
+                               0, stream, (const f16*)a.q, (const f16*)a.k_cache, (const f16*)a.v_cache,
+                               a.block_tables, a.context_lens, (f16*)a.out, a.o_part, a.m_part, a.l_part, counters,
+                               (int)a.hkv, (int)a.bs, bs_shift, (int)a.max_blocks, (int)a.num_blocks,
+                               (int)a.partition, (int)a.num_splits, a.sl2);
+        };
+        const bool many = gqa_waves<G>(a) == 4;
+        if constexpr (G == 8) {
+            if (many)
+                launch_mfma(std::integral_constant<int, 4>{});
+            else
+                launch_mfma(std::integral_constant<int, 8>{});
+        } else if (many)
             launch(std::integral_constant<int, 4>{});
+        else
+            launch(std::integral_constant<int, 8>{});
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.num_splits == 1 || counters) return e;

@@ -68,6 +68,16 @@ __device__ __forceinline__ f32x16 mfma32x32x16(f16x8 a, f16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// 16x16x32 f16 MFMA with fp32 accumulators (CDNA4).
+//   A (16 x 32): lane l holds row l%16 and 8 k values selected by l/16
+//   B (32 x 16): lane l holds col l%16 and the same 8 k values
+//   C (16 x 16): lane l holds col l%16, rows 4*(l/16) + r, r = 0..3
+// A and B select k by (lane / 16, element) in the same way, so any operand
+// pair loaded with one (group, element) -> k map multiplies correctly.
+__device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
 // Swap bits 2 and 3 of a lane/row index (an involution).  Used to line up the
 // MFMA accumulator row order with 8-element contiguous runs.
 __host__ __device__ constexpr int swap23(int x) { return (x & ~0xC) | ((x & 4) << 1) | ((x & 8) >> 1); }

@@ -74,8 +74,11 @@ def test_chunk_edges_head_groups(d, hq, hkv, partition):
 
 
 @pytest.mark.parametrize("bs", [8, 16, 32, 12])
-def test_block_sizes(bs):
-    assert run([300, 2000, 17], 8, 2, 128, bs=bs) < TOL[128]
+@pytest.mark.parametrize("hq", [8, 16])
+def test_block_sizes(bs, hq):
+    """Four and eight query heads per kv head (the dot-product and the
+    matrix-core kernels); pages of other than 16 tokens take the checked path."""
+    assert run([300, 2000, 17], hq, 2, 128, bs=bs) < TOL[128]
 
 
 def test_long_context_split():
@@ -102,7 +105,7 @@ def test_torch_baseline_matches():
     assert max_err(out, oracle.paged_decode_fp32(q, kc, vc, bt, cl)) < TOL[128]
 
 
-@pytest.mark.parametrize("d,hq,hkv", [(64, 4, 2), (128, 4, 4), (128, 16, 4), (64, 16, 2)])
+@pytest.mark.parametrize("d,hq,hkv", [(64, 4, 2), (128, 4, 4), (128, 16, 4), (64, 16, 2), (128, 16, 2)])
 def test_scale_argument(d, hq, hkv):
     """Explicit scales on both kernels, including large ones (a nearly one-hot
     softmax: the per-wave reference maximum keeps moving) and negative ones."""
@@ -112,6 +115,32 @@ def test_scale_argument(d, hq, hkv):
     for s in (0.5, -0.1, 0.0, 4.0, -30.0):
         out = ak.paged_decode(qd, kcd, vcd, btd, cld, 700, scale=s, partition_size=256)
         assert max_err(out, oracle.paged_decode_fp32(q, kc, vc, bt, cl, scale=s)) < TOL[d], s
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("hq", [4, 8, 16])
+def test_rising_scores_move_the_reference_max(d, hq):
+    """Scores shaped as a bump along the context (a triangle on one head dim,
+    0 -> 24 -> 0 nats) move every wave's reference maximum several times on
+    the way up, and one late key 6 nats above the peak moves it once more
+    (it then carries about three quarters of the softmax, the bump the rest):
+    each move rescales O and l of the heads in flight.  Two, four and eight
+    query heads per kv head, split and unsplit."""
+    lens, hkv = [3000, 777], 2
+    kc, vc, bt, cl = cache(lens, hkv, d, seed=31)
+    kc = kc.astype(np.float32)
+    for b, n in enumerate(lens):
+        t = np.arange(n)
+        kc[bt[b, t // 16], :, t % 16, 0] = (6.0 * (1.0 - np.abs(2.0 * t / n - 1.0)))[:, None]
+    kc[bt[0, 2900 // 16], :, 2900 % 16, 0] = 7.5
+    kc = kc.astype(np.float16)
+    q = (0.1 * np.random.default_rng(32).standard_normal((2, hq, d), dtype=np.float32)).astype(np.float16)
+    q[..., 0] = 4.0
+    qd, kcd, vcd, btd, cld = to_dev(q, kc, vc, bt, cl)
+    ref = oracle.paged_decode_fp32(q, kc, vc, bt, cl, scale=1.0)
+    for part in (256, 1 << 20):
+        out = ak.paged_decode(qd, kcd, vcd, btd, cld, max(lens), scale=1.0, partition_size=part)
+        assert max_err(out, ref) < TOL[d], part
 
 
 def test_errors_match_reference():
@@ -128,7 +157,7 @@ def test_errors_match_reference():
 # ------------------------------------------------ bit-exact page gathering --
 
 @pytest.mark.parametrize("d,bs,group", [(128, 16, 1), (64, 8, 1), (128, 32, 1), (128, 16, 4), (128, 16, 2),
-                                        (64, 16, 8)])
+                                        (64, 16, 8), (128, 16, 8), (128, 32, 8)])
 def test_gather_reads_exact_token(d, bs, group):
     """Each (sequence, kv head) attends to one chosen token only (its key gets a
     +64 score, every other key -64, scale 1): the output must be that token's V
