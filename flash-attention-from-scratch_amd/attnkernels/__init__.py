@@ -107,7 +107,7 @@ def _sm_count(device_index):
 # is chosen from max_context_len alone (reading the lengths would cost a host
 # sync), so the rule must hold for uniform, mixed-length and skewed batches.
 # The MI355X split-K ablation of ``attnkernels.benchsuite`` (every power-of-two
-# partition; 12 uniform, 5 mixed-length and 2 skewed batches (one long sequence
+# partition; 16 uniform, 5 mixed-length and 3 skewed batches (one long sequence
 # among short ones) over one, four and eight query heads per kv head;
 # results/mi355x.md), with the splits merged in the decode kernel, sets the
 # constants:
@@ -117,13 +117,17 @@ def _sm_count(device_index):
 #     merge) for its share of the bytes;
 #   * splits of at most 4 chunks (1024 tokens): a long sequence among short
 #     ones (which the rule cannot see) is then cut into enough splits that it
-#     does not finish long after the rest;
+#     does not finish long after the rest.  Uniform batches of 8-16 sequences
+#     would take larger splits (3-10% faster at 2048-4096 tokens with eight
+#     query heads per kv head), but 2048-token splits cost the skewed batches
+#     with four and eight query heads per kv head 10-11% (21-27% with 16 and
+#     32 sequences);
 #   * no split once B * Hkv reaches 2 workgroups per CU and the context is at
 #     most 32 chunks (8192 tokens): the batch alone fills the GPU;
 #   * tokens per split a power-of-two number of chunks.
-# Together they reach 97% of the best partition on average and >= 85% in every
-# case (the previous rule, 8 per CU with 1024-token splits and no split at 2
-# per CU: 88% and 21%, on the skewed batch).
+# Together they reach 96.5% of the best partition on average and >= 85% in
+# every case (the previous rule, 8 per CU with 1024-token splits and no split
+# at 2 per CU: 87% and 21%, on a skewed batch).
 DECODE_WG_PER_CU = 1
 DECODE_MIN_CHUNKS = 1
 DECODE_MAX_SPLIT_CHUNKS = 4
