@@ -125,7 +125,7 @@ def _sm_count(device_index):
 #   * no split once B * Hkv reaches 2 workgroups per CU and the context is at
 #     most 32 chunks (8192 tokens): the batch alone fills the GPU;
 #   * tokens per split a power-of-two number of chunks.
-# Together they reach 96.5% of the best partition on average and >= 85% in
+# Together they reach 96.5-97% of the best partition on average and >= 85% in
 # every case (the previous rule, 8 per CU with 1024-token splits and no split
 # at 2 per CU: 87% and 21%, on a skewed batch).
 DECODE_WG_PER_CU = 1
