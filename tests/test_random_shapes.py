@@ -5,7 +5,9 @@ one at a time; this sweep draws combinations of them: odd batch x head
 counts, lengths around the tile sizes, both head sizes, causal or not,
 explicit scales, GQA ratios and variable lengths for prefill; head groups
 1-8, page sizes 8/12/16/32, random partitions, ragged contexts and
-out-of-range page ids for decode.  Sizes stay small enough for the oracle.
+out-of-range page ids for decode, plus a sweep that always takes eight query
+heads per kv head (the matrix-core decode kernel; pages of 48 tokens as
+well).  Sizes stay small enough for the oracle.
 """
 import numpy as np
 import pytest
@@ -17,7 +19,7 @@ from conftest import TOL, max_err
 
 pytestmark = pytest.mark.gpu
 
-N_PREFILL, N_DECODE = 24, 32
+N_PREFILL, N_DECODE, N_DECODE_EIGHT = 24, 32, 12
 
 
 def _prefill_case(i):
@@ -65,23 +67,33 @@ def test_prefill_random_shape(i):
     assert max_err(out, ref) < TOL[d], c
 
 
-def _decode_case(i):
-    rng = np.random.default_rng(3000 + i)
+def _decode_case(i, eight=False):
+    """Seeded random decode shape; with eight=True always eight query heads per
+    kv head (the matrix-core kernel) and more out-of-range pages."""
+    rng = np.random.default_rng((5000 if eight else 3000) + i)
     d = int(rng.choice([64, 128]))
     hkv = int(rng.choice([1, 2, 4, 8]))
-    g = int(rng.choice([1, 2, 4, 8]))
-    bs = int(rng.choice([16, 16, 8, 32, 12]))
+    g = 8 if eight else int(rng.choice([1, 2, 4, 8]))
+    bs = int(rng.choice([16, 16, 8, 32, 12] + ([48] if eight else [])))
     b = int(rng.integers(1, 7))
     hi = int(rng.choice([40, 700, 3000]))
     lens = [int(x) for x in rng.integers(1, hi + 1, size=b)]
     part = None if rng.random() < 0.4 else 256 * int(rng.integers(1, 9))
-    bad = rng.random() < 0.25
-    return dict(d=d, hkv=hkv, hq=hkv * g, bs=bs, lens=lens, part=part, bad=bad, seed=4000 + i)
+    bad = rng.random() < (0.4 if eight else 0.25)
+    return dict(d=d, hkv=hkv, hq=hkv * g, bs=bs, lens=lens, part=part, bad=bad, seed=(6000 if eight else 4000) + i)
 
 
 @pytest.mark.parametrize("i", range(N_DECODE))
 def test_decode_random_shape(i):
-    c = _decode_case(i)
+    _check_decode_case(_decode_case(i))
+
+
+@pytest.mark.parametrize("i", range(N_DECODE_EIGHT))
+def test_decode_random_shape_eight_heads(i):
+    _check_decode_case(_decode_case(i, eight=True))
+
+
+def _check_decode_case(c):
     print(c, flush=True)
     kc, vc, bt, cl = oracle.make_paged_cache(c["lens"], c["hkv"], c["d"], block_size=c["bs"], extra_blocks=3,
                                              seed=c["seed"])
