@@ -4,8 +4,8 @@ graph capture (torch.cuda.graph, global capture mode).  No kernel of the
 library runs before it; the inputs are made with torch.  The replays must
 equal ak_paged_decode_fused (the same kernels with a caller workspace) bit for
 bit, and free device memory must not change across the replays after the
-first.  Prints one JSON
-line."""
+first.  argv[1]: query heads (32: four per kv head, the dot-product kernel;
+64: eight, the matrix-core kernel).  Prints one JSON line."""
 import ctypes
 import json
 import sys
@@ -24,7 +24,8 @@ def main():
     lib.ak_paged_decode_workspace_size.restype = ctypes.c_size_t
     lib.ak_paged_decode_fused.argtypes = [vp] * 6 + [i64] * 8 + [f64, i64, vp, ctypes.c_size_t, vp, i64, vp]
     lib.ak_paged_decode_noalloc.argtypes = [vp] * 6 + [i64] * 8 + [f64, i64, vp]
-    lens, hq, hkv, d, bs, part = [3000, 1200, 40], 32, 8, 128, 16, 256
+    hq = int(sys.argv[1]) if len(sys.argv) > 1 else 32
+    lens, hkv, d, bs, part = [3000, 1200, 40], 8, 128, 16, 256
     nblk = [-(-n // bs) for n in lens]
     pool = sum(nblk) + 3
     g = torch.Generator(device="cuda").manual_seed(5)

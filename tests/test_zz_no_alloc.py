@@ -143,13 +143,17 @@ def test_noalloc_under_graph_capture_replays_bit_identically(lib):
         torch.cuda.synchronize()
 
 
-def test_noalloc_first_call_on_the_device_inside_a_graph_capture():
+@pytest.mark.parametrize("hq", [32, 64])
+def test_noalloc_first_call_on_the_device_inside_a_graph_capture(hq):
     """In a fresh process, the library's first call on the device is a
-    noalloc call inside a graph capture (the symbol lookup and module load
-    happen under capture); replays equal the fused entry point bit for bit and,
-    after the graph's first launch, leave free device memory unchanged."""
+    noalloc call inside a graph capture (the symbol lookup, the module load and
+    the grouped-query kernel's occupancy query happen under capture); replays
+    equal the fused entry point bit for bit and, after the graph's first
+    launch, leave free device memory unchanged.  Four and eight query heads
+    per kv head (the dot-product and the matrix-core kernel)."""
     helper = ROOT / "tests" / "noalloc_capture_first.py"
-    r = subprocess.run([sys.executable, str(helper)], capture_output=True, text=True, timeout=100)
+    print(f"fresh process, hq={hq}", flush=True)
+    r = subprocess.run([sys.executable, str(helper), str(hq)], capture_output=True, text=True, timeout=100)
     print(r.stdout, r.stderr[-2000:], flush=True)
     assert r.returncode == 0
     res = json.loads(r.stdout.strip().splitlines()[-1])
