@@ -996,15 +996,49 @@ paged_decode_gqa_mfma_kernel(const f16* __restrict__ q, const f16* __restrict__ 
                 vb[r] = __builtin_nontemporal_load(reinterpret_cast<const vrow_t*>(vpb + voff[r]));
             }
             const int tn = t0 + stride;
-            if (tn + T::TOK <= end) {
+            if (tn < end) {  // the next pair's page ids (page B only if it holds a token)
                 spa = bt[uniform(tn >> 4)];
-                spb = bt[uniform((tn >> 4) + 1)];
+                spb = tn + 16 < end ? bt[uniform((tn >> 4) + 1)] : -1;
             }
             if (balance) progress_priority(t0 - start, end - start);
             step(ka, kb, va, vb, unused, std::false_type{});
             t0 = tn;
         }
         __builtin_amdgcn_s_setprio(0);
+        // The pair that holds the end of the context: the same page-base loads
+        // with the page ids already loaded, rows past the end left zero and
+        // masked out of the softmax.  (Through the checked path below, each
+        // lane would look up its 10 token rows' page ids first: one more
+        // dependent memory round trip for every sequence.)
+        const bool hasb = t0 + 16 < end;
+        if (fast_bs && t0 < end && t0 + T::TOK > end && (unsigned)spa < (unsigned)num_blocks &&
+            (!hasb || (unsigned)spb < (unsigned)num_blocks)) {
+            f16x8 ka[KS], kb[KS];
+            vrow_t va[4], vb[4];
+            bool valid[8];
+            const int pb = hasb ? spb : spa;  // no row of page B is read when it holds no token
+            const char* kpa = reinterpret_cast<const char*>(kc + (size_t)spa * page_stride);
+            const char* vpa = reinterpret_cast<const char*>(vc + (size_t)spa * page_stride);
+            const char* kpb = reinterpret_cast<const char*>(kc + (size_t)pb * page_stride);
+            const char* vpb = reinterpret_cast<const char*>(vc + (size_t)pb * page_stride);
+            const bool ka_ok = t0 + n < end, kb_ok = t0 + 16 + n < end;
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                ka[s] = ka_ok ? __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(kpa + koff[s])) : f16x8{};
+                kb[s] = kb_ok ? __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(kpb + koff[s])) : f16x8{};
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                valid[r] = t0 + 4 * g + r < end;
+                valid[r + 4] = t0 + 16 + 4 * g + r < end;
+                va[r] = valid[r] ? __builtin_nontemporal_load(reinterpret_cast<const vrow_t*>(vpa + voff[r]))
+                                 : vrow_t{};
+                vb[r] = valid[r + 4] ? __builtin_nontemporal_load(reinterpret_cast<const vrow_t*>(vpb + voff[r]))
+                                     : vrow_t{};
+            }
+            step(ka, kb, va, vb, valid, std::true_type{});
+            t0 += stride;
+        }
     }
     // The rest (context tail, out-of-range page ids, pages not of 16 tokens):
     // every token row located on its own; rows that are not read are zeros.
