@@ -99,8 +99,8 @@ def test_decode_partition_default_is_near_the_measured_optimum(monkeypatch):
     power-of-two partition, uniform, mixed and skewed context lengths, one,
     four and eight query heads per kv head), a partition within 16% of the
     fastest one in every case (the worst case, one 32k sequence among 31 short
-    ones with 32 kv heads, read 84.7%, 85.0%, 85.6% and 85.1% of the best in
-    four runs of the suite) and within 4% on average (96.5-97% in the last two: with
+    ones with 32 kv heads, read 84.7-85.7% of the best in five runs of the
+    suite) and within 4% on average (96.5-97% in the last three: with
     eight heads per kv head the matrix-core kernel runs uniform batches of
     8-16 sequences x 8192 tokens 3-10% faster with 2048-4096-token splits, but
     2048-token splits cost the skewed batches with head groups 10-11%, so the
