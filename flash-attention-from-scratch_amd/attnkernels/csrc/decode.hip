@@ -265,12 +265,12 @@ paged_decode_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const
             pg[u] = t < lim ? bt[pi] : -1;
         }
     };
-    // The context length, q and the first chunk's page ids are loaded together:
+    // The context length and the first chunk's page ids are loaded together:
     // the page loads are bounded by the table row, not by the (not yet known)
-    // context length, which only masks them afterwards.
+    // context length, which only masks them afterwards.  q follows the context
+    // check, so that a workgroup past a short context (most of a skewed
+    // batch's grid) exits after one round trip.
     const int ctx_raw = ctx_lens[b];
-    // q of this head, raw fp16 (scaled after the dot product)
-    const f16x8 qv = *reinterpret_cast<const f16x8*>(q + ((size_t)b * hq + kvh) * D + li * 8);
     const int stride = T::NW * T::TOK;
     int pg[T::U];
     load_pages(start + w * T::TOK, min(start + partition, max_tok), pg);
@@ -284,6 +284,8 @@ paged_decode_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const
         return;
     }
     const int end = min(ctx, start + partition);
+    // q of this head, raw fp16 (scaled after the dot product)
+    const f16x8 qv = *reinterpret_cast<const f16x8*>(q + ((size_t)b * hq + kvh) * D + li * 8);
 
     float m[G] = {-INFINITY}, l[G] = {0.f}, acc[G][8] = {};
     const size_t page_stride = (size_t)hkv * bs * D;
@@ -553,10 +555,6 @@ paged_decode_gqa_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, c
         }
     };
     const int ctx_raw = ctx_lens[b];
-    f16x8 qv[G];  // register a: query head a ^ fh
-#pragma unroll
-    for (int a = 0; a < G; ++a)
-        qv[a] = *reinterpret_cast<const f16x8*>(q + ((size_t)b * hq + kvh * G + (a ^ fh)) * D + li * 8);
     const int stride = T::NW * T::TOK;
     int pg[U];
     const bool fast_bs = bs == T::TOK;
@@ -572,6 +570,12 @@ paged_decode_gqa_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, c
         return;
     }
     const int end = min(ctx, start + partition);
+    // q after the context check (a workgroup past a short context exits after
+    // one round trip)
+    f16x8 qv[G];  // register a: query head a ^ fh
+#pragma unroll
+    for (int a = 0; a < G; ++a)
+        qv[a] = *reinterpret_cast<const f16x8*>(q + ((size_t)b * hq + kvh * G + (a ^ fh)) * D + li * 8);
 
     // Per-wave reference max of this lane's head (fh), this lane's share of l
     // for that head, and the accumulators (register a: head a ^ fh, dims
@@ -860,16 +864,6 @@ paged_decode_gqa_mfma_kernel(const f16* __restrict__ q, const f16* __restrict__ 
     const int* bt = block_tables + (size_t)b * max_blocks;
     const int max_tok = max_blocks * bs;
     const int ctx_raw = ctx_lens[b];
-
-    // Q^T fragments: head n (zeros for n >= G), dims 32 s + 8 g .. +7.
-    f16x8 qf[KS];
-#pragma unroll
-    for (int s = 0; s < KS; ++s) qf[s] = f16x8{};
-    if (n < G) {
-        const f16* qrow = q + ((size_t)b * hq + kvh * G + n) * D + 8 * g;
-#pragma unroll
-        for (int s = 0; s < KS; ++s) qf[s] = *reinterpret_cast<const f16x8*>(qrow + 32 * s);
-    }
     const int stride = NW * T::TOK;
     const bool fast_bs = bs == 16;
     int t0 = start + w * T::TOK;
@@ -887,6 +881,18 @@ paged_decode_gqa_mfma_kernel(const f16* __restrict__ q, const f16* __restrict__ 
         return;
     }
     const int end = min(ctx, start + partition);
+
+    // Q^T fragments: head n (zeros for n >= G), dims 32 s + 8 g .. +7; loaded
+    // after the context check, so that a workgroup past a short context (most
+    // of a skewed batch's grid) exits after one round trip.
+    f16x8 qf[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qf[s] = f16x8{};
+    if (n < G) {
+        const f16* qrow = q + ((size_t)b * hq + kvh * G + n) * D + 8 * g;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) qf[s] = *reinterpret_cast<const f16x8*>(qrow + 32 * s);
+    }
 
     // Reference max of head n (the same in the head's four lanes), this
     // lane's share of l for head n, and acc[j][r]: head 4g + r, dim DPL n + j.
