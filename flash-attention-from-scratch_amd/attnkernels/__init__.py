@@ -107,7 +107,7 @@ def _sm_count(device_index):
 # is chosen from max_context_len alone (reading the lengths would cost a host
 # sync), so the rule must hold for uniform, mixed-length and skewed batches.
 # The MI355X split-K ablation of ``attnkernels.benchsuite`` (every power-of-two
-# partition; 16 uniform, 5 mixed-length and 3 skewed batches (one long sequence
+# partition; 19 uniform, 6 mixed-length and 5 skewed batches (one long sequence
 # among short ones) over one, four and eight query heads per kv head;
 # results/mi355x.md), with the splits merged in the decode kernel, sets the
 # constants:
@@ -124,37 +124,58 @@ def _sm_count(device_index):
 #     32 sequences);
 #   * no split once B * Hkv reaches 2 workgroups per CU and the context is at
 #     most 32 chunks (8192 tokens): the batch alone fills the GPU;
+#   * with that many blocks and a longer context, splits sized so that one
+#     sequence of max_context_len spreads its Hkv blocks over about 2
+#     workgroups per CU (2 * CUs / Hkv splits, at least 2 chunks, not capped
+#     at 4): if it is one long sequence among short ones, the short ones fill
+#     the GPU and the long one ends with them.  That gives 512 tokens for
+#     Hkv=8 at 16384 and 32768 tokens, 1024 and 2048 for Hkv=32.  The skewed
+#     batches with Hkv=8 run fastest at 256-512 tokens (1024 reads 73-87% of
+#     the best), uniform and mixed ones at 1024-16384 (512 reads 79-94% over
+#     three runs); a floor of 1 chunk would cost the uniform ones 14-26%;
 #   * tokens per split a power-of-two number of chunks.
-# Together they reach 96.5-97% of the best partition on average and >= 85% in
-# every case (the previous rule, 8 per CU with 1024-token splits and no split
-# at 2 per CU: 87% and 21%, on a skewed batch).
+# Together they reach 97% of the best partition on average and 88% in the
+# worst case in the committed ablation (without the long-context clause 95%
+# and 74%; the previous rule, 8 per CU with 1024-token splits and no split at
+# 2 per CU: 85% and 19%, on a skewed batch).
 DECODE_WG_PER_CU = 1
 DECODE_MIN_CHUNKS = 1
 DECODE_MAX_SPLIT_CHUNKS = 4
 DECODE_NO_SPLIT_BLOCKS_PER_CU = 2
 DECODE_NO_SPLIT_MAX_CHUNKS = 32
+DECODE_LONG_WG_PER_CU = 2
+DECODE_LONG_MIN_CHUNKS = 2
 REFERENCE_WG_PER_SM = 4
 
 
 def decode_partition(batch, num_kv_heads, max_context_len, device=None, wg_per_cu=DECODE_WG_PER_CU,
                      min_chunks=DECODE_MIN_CHUNKS, no_split_blocks_per_cu=DECODE_NO_SPLIT_BLOCKS_PER_CU,
                      no_split_max_chunks=DECODE_NO_SPLIT_MAX_CHUNKS, max_split_chunks=DECODE_MAX_SPLIT_CHUNKS,
-                     pow2_chunks=True):
+                     pow2_chunks=True, long_wg_per_cu=DECODE_LONG_WG_PER_CU,
+                     long_min_chunks=DECODE_LONG_MIN_CHUNKS):
     """Tokens per split for paged_decode: enough splits for about ``wg_per_cu``
     workgroups per CU in total, at least ``min_chunks`` and at most
     ``max_split_chunks`` 256-token chunks per split (a power of two of them if
     ``pow2_chunks``), and one split once ``batch * num_kv_heads`` reaches
     ``no_split_blocks_per_cu`` per CU with at most ``no_split_max_chunks``
-    chunks of context (reference attnkernels/__init__.py:93-101, whose rule is
+    chunks of context; with that many blocks and a longer context, enough
+    splits for ``long_wg_per_cu`` workgroups per CU from one sequence's kv
+    heads, of at least ``long_min_chunks`` chunks (reference attnkernels/__init__.py:93-101, whose rule is
     ``wg_per_cu=REFERENCE_WG_PER_SM, min_chunks=1, no_split_blocks_per_cu=None,
     max_split_chunks=None, pow2_chunks=False``)."""
     dev = torch.cuda.current_device() if device is None else device
     blocks = batch * num_kv_heads
     cus = _sm_count(dev)
     max_chunks = -(-max_context_len // CHUNK)
-    if (no_split_blocks_per_cu is not None and blocks >= no_split_blocks_per_cu * cus
-            and (no_split_max_chunks is None or max_chunks <= no_split_max_chunks)):
-        return max(1, max_chunks) * CHUNK
+    if no_split_blocks_per_cu is not None and blocks >= no_split_blocks_per_cu * cus:
+        if no_split_max_chunks is None or max_chunks <= no_split_max_chunks:
+            return max(1, max_chunks) * CHUNK
+        if long_wg_per_cu is not None:
+            splits = -(-int(long_wg_per_cu) * cus // num_kv_heads)
+            chunks = max(int(long_min_chunks), -(-max_chunks // splits))
+            if pow2_chunks:
+                chunks = 1 << (chunks - 1).bit_length()
+            return chunks * CHUNK
     want = -(-int(wg_per_cu) * cus // blocks)
     splits = max(1, min(want, -(-max_chunks // int(min_chunks))))
     chunks = -(-max_chunks // splits)

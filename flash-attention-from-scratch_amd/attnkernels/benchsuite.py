@@ -264,15 +264,17 @@ ABLATION_HEADS = ((32, 8), (32, 32), (64, 8))
 
 
 def ablation_builders(quick, status, max_kv_gb):
+    # the last of each head shape: B * Hkv >= 2 per CU with more than 8192 tokens
     uniform = {(32, 8): ((1, 4096), (1, 16384), (1, 32768), (2, 4096), (4, 8192), (16, 4096), (16, 8192), (64, 1024),
-                         (64, 4096)),
-               (32, 32): ((8, 32768), (16, 8192), (64, 4096)),
-               (64, 8): ((1, 32768), (8, 8192), (16, 8192), (64, 4096))}
-    mixed = {(32, 8): ((4, 512, 32768, 1), (16, 512, 32768, 2), (64, 1, 4096, 3)),
+                         (64, 4096), (64, 16384)),
+               (32, 32): ((8, 32768), (16, 8192), (64, 4096), (16, 16384)),
+               (64, 8): ((1, 32768), (8, 8192), (16, 8192), (64, 4096), (64, 16384))}
+    mixed = {(32, 8): ((4, 512, 32768, 1), (16, 512, 32768, 2), (64, 1, 4096, 3), (64, 512, 32768, 9)),
              (32, 32): ((64, 1, 4096, 4),),
              (64, 8): ((16, 512, 32768, 5),)}
     # one long sequence among many short ones, with B * Hkv >= 2 per CU
-    skewed = {(32, 8): ((64, 32768, 2048, 6),), (32, 32): ((32, 32768, 2048, 7),), (64, 8): ((64, 32768, 2048, 8),)}
+    skewed = {(32, 8): ((64, 32768, 2048, 6), (64, 16384, 2048, 10)), (32, 32): ((32, 32768, 2048, 7),),
+              (64, 8): ((64, 32768, 2048, 8), (64, 16384, 2048, 11))}
     if quick:
         uniform, mixed, skewed = {(32, 8): ((1, 8192),)}, {(32, 8): ((8, 512, 8192, 3),)}, {}
     for (hq, hkv), shapes in uniform.items():
