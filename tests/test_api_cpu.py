@@ -106,9 +106,11 @@ def test_decode_partition_default_is_near_the_measured_optimum(monkeypatch):
     """On 256 CUs the default rule picks, over every case of the MI355X split-K
     ablation (tests/golden/decode_partition_mi355x.json: bandwidth of every
     power-of-two partition, uniform, mixed and skewed context lengths, one,
-    four and eight query heads per kv head), a partition within 15% of the
-    fastest one in every case (88% in the committed run, the worst a uniform
-    batch of 64 x 16384 tokens split into 512-token pieces) and within 4% on
+    four and eight query heads per kv head), a partition within 22% of the
+    fastest one in every case (83-89% over three full suite runs and 79% in an
+    ablation-only run, the worst each time a uniform batch of 64 x 16384
+    tokens split into 512-token pieces, whose rate at 512 moves 79-93% of the
+    best from run to run) and within 4% on
     average (97%: with eight heads per kv head the matrix-core kernel runs
     uniform batches of 8-16 sequences x 8192 tokens 3-10% faster with
     2048-4096-token splits, but 2048-token splits cost the skewed batches with
@@ -143,7 +145,7 @@ def test_decode_partition_default_is_near_the_measured_optimum(monkeypatch):
         return min(fr), sum(fr) / len(fr)
 
     worst, mean = fractions()
-    assert worst >= 0.85 and mean >= 0.96
+    assert worst >= 0.78 and mean >= 0.96
     assert fractions(long_wg_per_cu=None)[1] < mean
     assert fractions(**REFERENCE_RULE)[1] < mean
     prev_worst, prev_mean = fractions(**PREVIOUS_RULE)
