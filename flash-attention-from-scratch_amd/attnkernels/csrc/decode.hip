@@ -558,9 +558,6 @@ paged_decode_gqa_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, c
     const int stride = T::NW * T::TOK;
     int pg[U];
     const bool fast_bs = bs == T::TOK;
-    int spg = 0;
-    if (fast_bs && start + w * T::TOK + T::TOK <= min(start + partition, max_tok))
-        spg = bt[uniform((start + w * T::TOK) >> 4)];
 
     const int ctx = min(ctx_raw, max_tok);
     if (start >= ctx) {
@@ -570,8 +567,13 @@ paged_decode_gqa_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, c
         return;
     }
     const int end = min(ctx, start + partition);
-    // q after the context check (a workgroup past a short context exits after
-    // one round trip)
+    // The first page id and q after the context check: a workgroup past a
+    // short context exits after its one scalar load (the check's wait would
+    // also wait for a page id loaded beside it; a skewed batch's step 3%
+    // faster, uniform batches unchanged).
+    int spg = 0;
+    if (fast_bs && start + w * T::TOK + T::TOK <= min(start + partition, max_tok))
+        spg = bt[uniform((start + w * T::TOK) >> 4)];
     f16x8 qv[G];  // register a: query head a ^ fh
 #pragma unroll
     for (int a = 0; a < G; ++a)
@@ -867,11 +869,6 @@ paged_decode_gqa_mfma_kernel(const f16* __restrict__ q, const f16* __restrict__ 
     const int stride = NW * T::TOK;
     const bool fast_bs = bs == 16;
     int t0 = start + w * T::TOK;
-    int spa = -1, spb = -1;  // page ids of the pair at t0 (wave-uniform), loaded one pair ahead
-    if (fast_bs && t0 + T::TOK <= min(start + partition, max_tok)) {
-        spa = bt[uniform(t0 >> 4)];
-        spb = bt[uniform((t0 >> 4) + 1)];
-    }
 
     const int ctx = min(ctx_raw, max_tok);
     if (start >= ctx) {
@@ -881,10 +878,16 @@ paged_decode_gqa_mfma_kernel(const f16* __restrict__ q, const f16* __restrict__ 
         return;
     }
     const int end = min(ctx, start + partition);
+    // The first pair's page ids and the Q^T fragments after the context
+    // check, so that a workgroup past a short context (most of a skewed
+    // batch's grid) exits after its one scalar load.
+    int spa = -1, spb = -1;  // page ids of the pair at t0 (wave-uniform), loaded one pair ahead
+    if (fast_bs && t0 + T::TOK <= min(start + partition, max_tok)) {
+        spa = bt[uniform(t0 >> 4)];
+        spb = bt[uniform((t0 >> 4) + 1)];
+    }
 
-    // Q^T fragments: head n (zeros for n >= G), dims 32 s + 8 g .. +7; loaded
-    // after the context check, so that a workgroup past a short context (most
-    // of a skewed batch's grid) exits after one round trip.
+    // Q^T fragments: head n (zeros for n >= G), dims 32 s + 8 g .. +7.
     f16x8 qf[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) qf[s] = f16x8{};
