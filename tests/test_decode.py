@@ -51,6 +51,29 @@ def test_uniform(d, heads, ctx):
 
 RAGGED = [1, 17, 255, 256, 257, 999, 4097, 33]
 
+# One long sequence among sequences of 0-17 tokens: at P = 256 its 36 splits
+# go to the reduce kernel and all but the first of each short sequence's 36
+# split workgroups are past its context, so they exit after loading its length
+# (the page ids and q are loaded after that check); at P = 512 and 2048 the
+# splits merge in the decode kernel.
+SKEWED = [9000, 1, 3, 16, 1, 0, 2, 17, 1, 5]
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("heads", [(8, 8), (16, 8), (32, 8), (64, 8)])
+@pytest.mark.parametrize("partition", [256, 512, 2048])
+def test_skewed_batch_of_mostly_empty_splits(d, heads, partition):
+    kc, vc, bt, cl = cache(SKEWED, heads[1], d, seed=41)
+    q = rand_q(len(SKEWED), heads[0], d, 42)
+    qd, kcd, vcd, btd, cld = to_dev(q, kc, vc, bt, cl)
+    out = ak.paged_decode(qd, kcd, vcd, btd, cld, max(SKEWED), partition_size=partition)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    assert float(out[SKEWED.index(0)].abs().max()) == 0.0  # no context: a zero row
+    live = [i for i, c in enumerate(SKEWED) if c > 0]
+    ref = oracle.paged_decode_fp32(q[live], kc, vc, bt[live], cl[live])
+    assert max_err(out[live], ref) < TOL[d]
+
 
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("partition", [None, 256, 1024, 1 << 20])
